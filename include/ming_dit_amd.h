@@ -1,0 +1,163 @@
+/*
+ * ming_dit_amd.h -- the C-ABI of the MI355X-native DiT block-projection
+ * path of Ming-Image (a drop-in for the reference's ming-dit / ming-ops /
+ * ming-quant-family seams, tgo-app-dev/vpipe-ming-image).
+ *
+ * Plain C: opaque handles, plain pointers and sizes, integer status codes,
+ * no exceptions across the boundary. Activations are bf16 bit patterns
+ * (uint16_t) in device memory, token-major with an explicit row stride in
+ * ELEMENTS (the reference passes element offsets, ming-dit.cc:1763; a
+ * caller adds them to the pointer). One caller thread per context; work
+ * is enqueued in order on the context's HIP stream and entry points return
+ * without waiting unless they say otherwise.
+ *
+ * Status: 0 ok, > 0 error (ming_last_error() says why, per thread),
+ * < 0 a cooperative stop (ming-dit.h:170-189: empty result, empty error).
+ */
+#ifndef MING_DIT_AMD_H
+#define MING_DIT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MING_ABI_VERSION 1
+
+/* Runtime-LoRA slots: lora::Stack::kMax (ming-dit.h:117) and the eight
+ * `lora`..`lora8` keys (ming-model-config-stage.h:37-56). */
+#define MING_MAX_LORA_SLOTS 8
+/* Largest adapter rank one slot binds. */
+#define MING_MAX_LORA_RANK 512
+
+enum {
+  MING_OK = 0,
+  MING_ERR_ARG = 1,     /* a null handle/pointer or an out-of-range value */
+  MING_ERR_SHAPE = 2,   /* a shape the path does not take */
+  MING_ERR_HIP = 3,     /* the HIP runtime reported an error */
+  MING_ERR_ALLOC = 4,   /* device memory could not be allocated */
+  MING_ERR_KERNEL = 5,  /* a kernel failed validation at context creation */
+  MING_ERR_STATE = 6,   /* the call does not fit the object's state */
+  MING_STOPPED = -1     /* a cooperative stop: not an error */
+};
+
+typedef struct ming_ctx ming_ctx;
+typedef struct ming_qweight ming_qweight;
+
+/* What the context DISPATCHED since its last reset, counted at the
+ * dispatch site (the reference's DitEngagement, ming-dit.h:55-103): a
+ * route that is configured but never ran passes every numeric bar, so
+ * tests assert these before accuracy. */
+typedef struct ming_engagement {
+  int64_t gemm_q4;      /* quantized w4 projections (gemm_qmm, w4) */
+  int64_t gemm_q8;      /* quantized w8 projections (gemm_qmm, w8) */
+  int64_t gemm_dense;   /* dense bf16 projections */
+  int64_t lora_proj;    /* projections that carried >= 1 live adapter */
+  int64_t lora_xa;      /* stacked x.A GEMMs launched */
+  int64_t rmsnorm;
+  int64_t qk_norm_rope;
+  int64_t rope_table;
+  int64_t attention;
+  int64_t elementwise;
+  uint64_t gemm_flops;  /* 2*M*N*K + sum_live 2*M*r*(K+N) per projection */
+} ming_engagement;
+
+/* Last error of the CALLING thread; "" when the last call succeeded. */
+const char* ming_last_error(void);
+int ming_abi_version(void);
+
+/* ---- context --------------------------------------------------------------
+ * Binds a device and a stream (NULL: the context creates and owns one).
+ * Every kernel the path dispatches is resolved and VALIDATED here, and a
+ * missing one refuses the context rather than degrading (the reference's
+ * load-time refusal, ming-dit.cc:1141-1235). */
+int ming_ctx_create(int device, void* hip_stream, ming_ctx** out);
+/* Refused (MING_ERR_STATE) while weights made on the context are alive. */
+int ming_ctx_destroy(ming_ctx* ctx);
+int ming_ctx_set_stream(ming_ctx* ctx, void* hip_stream);
+void* ming_ctx_stream(const ming_ctx* ctx);
+int ming_ctx_synchronize(ming_ctx* ctx);
+int ming_ctx_engagement(const ming_ctx* ctx, ming_engagement* out);
+int ming_ctx_reset_engagement(ming_ctx* ctx);
+
+/* ---- projection weights (the quant pack) ------------------------------------
+ * A quantized projection in the reference's pack layout (load_qw_,
+ * ming-dit.cc:802-831; pack detection 1115-1135): codes U32
+ * [N, K*bits/32] (unsigned codes, LSB-first within a word), scales and
+ * biases bf16 [N, K/group], w = scales*q + biases. bits 4 or 8, group 64,
+ * K % 64 == 0, N % 8 == 0. `src_on_device` 0 reads host memory. The
+ * weight is repacked into the kernels' resident tiled layout; the sources
+ * may be freed when the call returns. */
+int ming_qweight_create(ming_ctx* ctx, int N, int K, int bits, int group,
+                        const uint32_t* codes, const uint16_t* scales,
+                        const uint16_t* biases, int src_on_device,
+                        ming_qweight** out);
+/* A dense bf16 [N, K] projection (a dense checkpoint's `.weight`,
+ * to_elt_ at ming-dit.cc:795-800). */
+int ming_qweight_create_dense(ming_ctx* ctx, int N, int K, const uint16_t* w,
+                              int src_on_device, ming_qweight** out);
+/* Several projections over the SAME input fused along N (q|k|v;
+ * w1|w3): the output is their concatenation, each part keeping its own
+ * adapter bindings (part i = segment i). Parts must share K and bits, and
+ * every part but the last must have N % 256 == 0. At most 4 parts. The
+ * parts stay valid and independent. */
+int ming_qweight_concat(ming_ctx* ctx, int n_parts,
+                        ming_qweight* const* parts, ming_qweight** out);
+int ming_qweight_destroy(ming_qweight* qw);
+/* 4, 8 or 16 (dense bf16); 0 on a null handle. */
+int ming_qweight_bits(const ming_qweight* qw);
+int ming_qweight_shape(const ming_qweight* qw, int* N, int* K, int* n_segments);
+
+/* ---- runtime LoRA, bound at load (bind_loras_, ming-dit.cc:2918-3005) -------
+ * Binds slot `slot`'s factors to segment `segment` of a projection:
+ * A [rank, K] bf16 (down), B [N_seg, rank] bf16 (up), and `fold` the
+ * adapter's alpha/rank (the factor the reference folds into A). The delta
+ * is fold * scale * B (A x). Wrong shapes are refused (MING_ERR_SHAPE),
+ * which the model level turns into refusing the WHOLE slot. */
+int ming_qweight_bind_lora(ming_qweight* qw, int segment, int slot, int rank,
+                           const uint16_t* A, const uint16_t* B, float fold,
+                           int src_on_device);
+int ming_qweight_unbind_lora(ming_qweight* qw, int segment, int slot);
+/* Rank bound at (segment, slot), 0 when unbound. */
+int ming_qweight_lora_rank(const ming_qweight* qw, int segment, int slot);
+
+/* ---- the projection (lin, ming-dit.cc:1763-1771) -----------------------------
+ * y[M, N] = x[M, K] . W^T + sum over live slots of
+ *           fold * scales[slot] * B_slot (A_slot x)
+ * `scales` holds MING_MAX_LORA_SLOTS live strengths (NULL: all 0). A slot
+ * is live when it is bound on the segment AND its strength is non-zero;
+ * strength 0 encodes nothing at all, so an all-zero call is bit-identical
+ * to an unadapted one (ming-dit.h:150-154, ming-dit.cc:3015-3019).
+ * ldx, ldy in elements (>= K, >= N; multiples of 8). x and y device. */
+int ming_lin(ming_ctx* ctx, const ming_qweight* qw, const uint16_t* x,
+             int64_t ldx, uint16_t* y, int64_t ldy, int M,
+             const float* scales);
+
+/* ---- norms and rotary ----------------------------------------------------------
+ * rms (ming-dit.cc:1780-1787): y = bf16(x * rsqrt(mean(x^2)+eps) * w) per
+ * row of D (D % 8 == 0, D <= 8192); in place when x == y. */
+int ming_rmsnorm(ming_ctx* ctx, const uint16_t* x, int64_t ldx,
+                 const uint16_t* w, uint16_t* y, int64_t ldy, int rows, int D,
+                 float eps);
+/* The rotary tables of build_rope_ (ming-dit.cc:1443-1486) from device
+ * int32 positions [n] per axis: f32 cos/sin [n][head_dim/2], pairs split
+ * over the three axes as axes[0]/2, axes[1]/2, axes[2]/2, angles in f64. */
+int ming_rope_table(ming_ctx* ctx, const int32_t* pos_t, const int32_t* pos_h,
+                    const int32_t* pos_w, int n, const int* axes, int head_dim,
+                    double theta, float* cos_out, float* sin_out);
+/* qk-norm + RoPE, in place on token-major rows (ming-dit.cc:2083-2088):
+ * per head of 128, RMSNorm with wq / wk [128], then the interleaved-pair
+ * rotation with table row `row` (the caller offsets the tables by row0).
+ * q heads start at column q_col, k heads at k_col; n_heads each. */
+int ming_qk_norm_rope(ming_ctx* ctx, uint16_t* x, int64_t ld, int q_col,
+                      int k_col, int rows, int n_heads, int head_dim,
+                      const uint16_t* wq, const uint16_t* wk,
+                      const float* cos_t, const float* sin_t, float eps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MING_DIT_AMD_H */

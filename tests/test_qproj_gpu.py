@@ -1,0 +1,236 @@
+"""GPU parity of the projection path (ming_lin) against the CPU oracle.
+
+Bar (north_star): rel-L2 <= 2e-3 against the fp32 dequant+GEMM+LoRA
+reference, and bit-identity with the unadapted run when every strength is
+0. Engagement counters are asserted before accuracy (ming-dit.h:55-103).
+"""
+import numpy as np
+import pytest
+
+import ming_dit_amd as m
+from helpers import (CFG2_RANKS, CFG2_SCALES, bf16, empty_bf16, from_dev,
+                     make_lora, make_weight, randn, sync, to_dev)
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _qw(ctx, pack, bits):
+    if bits == 16:
+        return m.QWeight.dense(ctx, pack["w"])
+    return m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
+                               pack["biases"], bits)
+
+
+def _run(ctx, qw, x_dev, M, scales=None):
+    y = empty_bf16(M, qw.N)
+    sync()
+    ctx.lin(qw, x_dev, y, M, scales)
+    sync()
+    return from_dev(y)
+
+
+def _rel(orc, y_bf16, ref):
+    return orc.rel_l2(orc.bf16_to_f32(y_bf16), ref)
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+@pytest.mark.parametrize("M,N,K", [(300, 512, 640), (1, 264, 64),
+                                   (257, 256, 3840), (64, 1024, 192)])
+def test_base_projection_parity(ctx, orc, bits, M, N, K):
+    print(f"case bits={bits} M={M} N={N} K={K}", flush=True)
+    x = bf16(randn(1000 + M, (M, K)))
+    pack, w = make_weight(2000 + N, N, K, bits)
+    qw = _qw(ctx, pack, bits)
+    ctx.reset_engagement()
+    y = _run(ctx, qw, to_dev(x), M)
+    eng = ctx.engagement()
+    key = {4: "gemm_q4", 8: "gemm_q8", 16: "gemm_dense"}[bits]
+    assert eng[key] == 1 and eng["lora_proj"] == 0 and eng["lora_xa"] == 0
+    ref = orc.proj(x, w)
+    assert _rel(orc, y, ref) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_lora_eight_slots_parity(ctx, orc, bits):
+    """BASELINE config 2's adapter set on one projection."""
+    M, N, K = 320, 768, 1024
+    x = bf16(randn(11, (M, K)))
+    pack, w = make_weight(12, N, K, bits)
+    qw = _qw(ctx, pack, bits)
+    loras = []
+    for s, r in enumerate(CFG2_RANKS):
+        A, B = make_lora(100 + 2 * s, N, K, r)
+        qw.bind_lora(s, A, B)
+        loras.append((A, B, CFG2_SCALES[s]))
+    assert [qw.lora_rank(s) for s in range(8)] == list(CFG2_RANKS)
+    ctx.reset_engagement()
+    y = _run(ctx, qw, to_dev(x), M, CFG2_SCALES)
+    eng = ctx.engagement()
+    assert eng["lora_proj"] == 1 and eng["lora_xa"] == 1
+    ref = orc.proj(x, w, loras)
+    base = orc.proj(x, w)
+    rel = _rel(orc, y, ref)
+    assert rel <= TOL
+    # the adapter MOVED the output far past the bar (not a vacuous match)
+    assert orc.rel_l2(ref, base) > 10 * TOL
+
+
+def test_zero_strength_is_bit_identical(ctx, orc):
+    """All eight strengths 0 == the unadapted projection, memcmp
+    (ming-dit-test.cc:1249-1273)."""
+    M, N, K = 300, 512, 640
+    x = to_dev(bf16(randn(21, (M, K))))
+    pack, _ = make_weight(22, N, K, 4)
+    qw = _qw(ctx, pack, 4)
+    plain = _qw(ctx, pack, 4)
+    for s, r in enumerate(CFG2_RANKS):
+        A, B = make_lora(200 + 2 * s, N, K, r)
+        qw.bind_lora(s, A, B)
+    ctx.reset_engagement()
+    y0 = _run(ctx, qw, x, M, [0.0] * 8)
+    assert ctx.engagement()["lora_proj"] == 0
+    assert np.array_equal(y0, _run(ctx, plain, x, M))
+    assert np.array_equal(y0, _run(ctx, qw, x, M, None))
+
+
+def test_live_strength_change_and_back(ctx, orc):
+    """Strengths change between calls without rebinding, and going back
+    reproduces the first bits (ming-dit-test.cc:1257-1264)."""
+    M, N, K = 256, 512, 512
+    x = to_dev(bf16(randn(31, (M, K))))
+    pack, w = make_weight(32, N, K, 8)
+    qw = _qw(ctx, pack, 8)
+    A, B = make_lora(33, N, K, 16)
+    qw.bind_lora(0, A, B)
+    y1 = _run(ctx, qw, x, M, [0.8])
+    y2 = _run(ctx, qw, x, M, [-0.5])
+    y3 = _run(ctx, qw, x, M, [0.8])
+    assert np.array_equal(y1, y3)
+    assert not np.array_equal(y1, y2)
+    xh = from_dev(x)
+    assert _rel(orc, y2, orc.proj(xh, w, [(A, B, -0.5)])) <= TOL
+
+
+def test_slots_are_positional(ctx, orc):
+    """An adapter alone in slot 2 or slot 8 computes the bits it computes
+    alone in slot 1 (ming-dit-test.cc:1294-1339)."""
+    M, N, K = 200, 256, 384
+    x = to_dev(bf16(randn(41, (M, K))))
+    pack, _ = make_weight(42, N, K, 4)
+    A, B = make_lora(43, N, K, 32)
+    outs = []
+    for slot in (0, 1, 7):
+        qw = _qw(ctx, pack, 4)
+        qw.bind_lora(slot, A, B)
+        sc = [0.0] * 8
+        sc[slot] = 0.7
+        outs.append(_run(ctx, qw, x, M, sc))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+def test_two_halves_make_one(ctx, orc):
+    M, N, K = 128, 256, 256
+    x = to_dev(bf16(randn(51, (M, K))))
+    pack, _ = make_weight(52, N, K, 8)
+    A, B = make_lora(53, N, K, 16)
+    one = _qw(ctx, pack, 8)
+    one.bind_lora(0, A, B)
+    two = _qw(ctx, pack, 8)
+    two.bind_lora(0, A, B)
+    two.bind_lora(1, A, B)
+    y1 = _run(ctx, one, x, M, [1.0])
+    y2 = _run(ctx, two, x, M, [0.5, 0.5])
+    assert orc.rel_l2(orc.bf16_to_f32(y2), orc.bf16_to_f32(y1)) < 1e-3
+
+
+def test_fold_scales_the_delta(ctx, orc):
+    M, N, K = 96, 256, 256
+    xh = bf16(randn(61, (M, K)))
+    pack, w = make_weight(62, N, K, 4)
+    A, B = make_lora(63, N, K, 8)
+    qw = _qw(ctx, pack, 4)
+    qw.bind_lora(3, A, B, fold=2.0)   # alpha 16 / rank 8
+    y = _run(ctx, qw, to_dev(xh), M, [0, 0, 0, 0.5])
+    assert _rel(orc, y, orc.proj(xh, w, [(A, B, 1.0)])) <= TOL
+
+
+def test_fused_qkv_equals_separate(ctx, orc):
+    """q|k|v fused along N, each with its own adapters, gives the bits of
+    three separate projections."""
+    M, H, K = 300, 512, 512
+    x = to_dev(bf16(randn(71, (M, K))))
+    parts, sep = [], []
+    for i in range(3):
+        pack, _ = make_weight(72 + i, H, K, 4)
+        p = _qw(ctx, pack, 4)
+        A, B = make_lora(80 + 2 * i, H, K, 16 * (i + 1))
+        p.bind_lora(i, A, B)
+        parts.append(p)
+    fused = m.QWeight.concat(ctx, parts)
+    assert fused.N == 3 * H and fused.n_segments == 3
+    sc = [0.9, -0.4, 0.6]
+    ctx.reset_engagement()
+    yf = _run(ctx, fused, x, M, sc)
+    eng = ctx.engagement()
+    assert eng["lora_xa"] == 1 and eng["lora_proj"] == 3
+    for i, p in enumerate(parts):
+        yi = _run(ctx, p, x, M, sc)
+        assert np.array_equal(yf[:, i * H:(i + 1) * H], yi)
+
+
+def test_strided_rows_in_and_out(ctx, orc):
+    """Element strides on x and y (the reference's element offsets)."""
+    M, N, K = 130, 256, 256
+    xh = bf16(randn(91, (M, 2 * K)))
+    pack, w = make_weight(92, N, K, 8)
+    qw = _qw(ctx, pack, 8)
+    xd = to_dev(xh)
+    y = empty_bf16(M, 3 * N)
+    y.zero_()
+    sync()
+    ctx.lin(qw, xd[:, K:], y[:, N:], M, None, ldx=2 * K, ldy=3 * N)
+    sync()
+    yh = from_dev(y)
+    ref = orc.proj(np.ascontiguousarray(xh[:, K:]), w)
+    assert _rel(orc, np.ascontiguousarray(yh[:, N:2 * N]), ref) <= TOL
+    assert np.all(yh[:, :N] == 0) and np.all(yh[:, 2 * N:] == 0)
+
+
+def test_bad_shapes_are_refused(ctx):
+    pack, _ = make_weight(95, 64, 128, 4)
+    qw = _qw(ctx, pack, 4)
+    y = empty_bf16(8, 64)
+    x = empty_bf16(8, 128)
+    with pytest.raises(m.MingError):
+        ctx.lin(qw, x, y, 8, None, ldx=100)      # ldx < K
+    with pytest.raises(m.MingError):
+        qw.bind_lora(8, np.zeros((4, 128), np.uint16), np.zeros((64, 4), np.uint16))
+    with pytest.raises(m.MingError):      # bits 5 is not a pack
+        m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
+                            pack["biases"], 5)
+    with pytest.raises(m.MingError):      # K % 64 != 0
+        m.QWeight.dense(ctx, np.zeros((64, 96), np.uint16))
+
+
+def test_config1_full_size(ctx, orc):
+    """to_q w8g64, X [4096, 3840], one r16 slot at 0.8,
+    then 0 (memcmp with the unadapted run). The fp32 reference runs on a
+    row sample spread over every M tile."""
+    M, N, K = 4096, 3840, 3840
+    x = bf16(randn(1001, (M, K)))
+    w = randn(1002, (N, K), 0.02)
+    codes, sc, bi = orc.quantize(w, 8)
+    wd = orc.dequant(codes, sc, bi, 8)
+    A = bf16(randn(1003, (16, K), 1.0 / np.sqrt(K)))
+    B = bf16(randn(1004, (N, 16), 0.01))
+    qw = m.QWeight.quantized(ctx, codes, sc, bi, 8)
+    plain = m.QWeight.quantized(ctx, codes, sc, bi, 8)
+    qw.bind_lora(0, A, B)
+    xd = to_dev(x)
+    y = _run(ctx, qw, xd, M, [0.8])
+    rows = np.arange(0, M, 61)
+    ref = orc.proj(np.ascontiguousarray(x[rows]), wd, [(A, B, 0.8)])
+    assert _rel(orc, np.ascontiguousarray(y[rows]), ref) <= TOL
+    y0 = _run(ctx, qw, xd, M, [0.0])
+    assert np.array_equal(y0, _run(ctx, plain, xd, M))

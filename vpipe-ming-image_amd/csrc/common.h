@@ -1,0 +1,58 @@
+// Shared device helpers for the MI355X (gfx950) kernels of the DiT
+// block-projection path. Wave64 throughout; bf16 values travel as their
+// uint16 bit patterns.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ming {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t u) {
+  return __uint_as_float(u << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t u) {
+  return __uint_as_float(u & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float((uint32_t)h << 16);
+}
+
+// Round-to-nearest-even f32 -> bf16; NaN stays a quiet NaN (0x7fc0), the
+// generator's convention (ming-generator.cc:44-52).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// Two bf16 (one u32) -> two fp16 (one u32). Exact for every value inside
+// fp16's range, so the rounding mode of the packed conversion is moot.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u) {
+  auto h = __builtin_amdgcn_cvt_pkrtz(bf16_lo(u), bf16_hi(u));
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// Two f32 -> two fp16, round to nearest even.
+__device__ __forceinline__ uint32_t f32x2_to_f16x2_rne(float a, float b) {
+  _Float16 ha = (_Float16)a, hb = (_Float16)b;
+  return (uint32_t)__builtin_bit_cast(uint16_t, ha) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace ming

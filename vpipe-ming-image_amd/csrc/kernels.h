@@ -1,0 +1,93 @@
+// Host-side launch interface of the HIP kernels (internal to the library;
+// the public boundary is include/ming_dit_amd.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ming {
+
+// ---- quantized / dense projection GEMM with the LoRA tail ------------------
+//
+// y[m][n] = sum_k x[m][k] W[n][k]  (+ sum_r T[m][seg.t_col0 + r] B[n][r])
+//
+// W is resident in the tiled layout built by repack_* (K-tile major):
+//   bits 4:  codes[kt][n][8]  u32, nibble i of word j holds k = 8j + perm(i)
+//            with perm = {0,2,4,6,1,3,5,7}
+//   bits 8:  codes[kt][n][16] u32, byte i of word j holds k = 4j + i
+//   bits 16: dense bf16 w[n][k] (the checkpoint's own layout)
+//   sb[kt][n] = bf16 scale | bf16 bias << 16 (bits 4 and 8)
+// T is the LoRA intermediate [M][ldt] bf16 (already scaled), B the
+// segment's factors [N_seg][ldb] bf16, gathered per 16-wide rank group by
+// `grp` (B column / 16, or -1 for a zero group).
+constexpr int kQpBM = 256, kQpBN = 256, kQpBK = 64, kQpThreads = 256;
+constexpr int kMaxSeg = 4;
+constexpr int kMaxGroups = 256;   // 16-wide rank groups per call
+
+struct QprojSeg {
+  int n_begin;          // first output column of this segment
+  int n_end;
+  int t_col0;           // first T column of this segment's live ranks
+  int chunks;           // live rank chunks of 64 (0: no adapter)
+  int ldb;
+  int grp0;             // first entry of this segment in grp[]
+  const uint16_t* B;    // row (n - n_begin)
+};
+
+struct QprojArgs {
+  const uint16_t* x;
+  long long ldx;
+  const uint32_t* codes;
+  const uint32_t* sb;
+  const uint16_t* w16;
+  uint16_t* y;
+  long long ldy;
+  int M, N, K;
+  const uint16_t* t;
+  int ldt;
+  int nseg;
+  QprojSeg seg[kMaxSeg];
+  int16_t grp[kMaxGroups];
+};
+
+hipError_t launch_qproj(int bits, const QprojArgs& a, hipStream_t s);
+
+// T[m][c] = bf16(coef[c/16] * sum_k x[m][k] A[row(c)][k]) for c < n_cols,
+// row(c) = 16*grp[c/16] + c%16 (grp -1: a zero column). A is [R][K] bf16.
+struct LoraXaArgs {
+  const uint16_t* x;
+  long long ldx;
+  const uint16_t* A;
+  int K;
+  int M;
+  int n_cols;           // multiple of 64
+  uint16_t* t;
+  int ldt;
+  int16_t grp[kMaxGroups];
+  float coef[kMaxGroups];
+};
+hipError_t launch_lora_xa(const LoraXaArgs& a, hipStream_t s);
+
+// Repack the reference pack (codes [N][K*bits/32] u32 LSB-first,
+// scales/biases bf16 [N][K/64]) into the tiled resident layout.
+hipError_t launch_repack(int bits, const uint32_t* codes,
+                         const uint16_t* scales, const uint16_t* biases,
+                         int N, int K, uint32_t* codes_t, uint32_t* sb,
+                         hipStream_t s);
+
+// ---- norms and rotary --------------------------------------------------------
+hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
+                          uint16_t* y, long long ldy, int rows, int D,
+                          float eps, hipStream_t s);
+hipError_t launch_rope_table(const int32_t* pt, const int32_t* ph,
+                             const int32_t* pw, int n, int a0, int a1, int a2,
+                             int head_dim, double theta, float* cos_t,
+                             float* sin_t, hipStream_t s);
+hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
+                               int k_col, int rows, int n_heads,
+                               const uint16_t* wq, const uint16_t* wk,
+                               const float* cos_t, const float* sin_t,
+                               float eps, hipStream_t s);
+
+}  // namespace ming

@@ -1,0 +1,228 @@
+// RMSNorm and fused qk-norm + RoPE, the kernels that feed the projections.
+//
+// rmsnorm: y = bf16((x * 1/sqrt(mean(x^2) + eps)) * w), statistics in f32
+// (the host's rms_norm_fast_f16 as dispatched at ming-dit.cc:1780-1787).
+// One pass: each row is read once into registers (16-byte loads), reduced
+// across the lanes that own it with DPP/permute shuffles, scaled and
+// written back. HBM-bound: 4*D bytes per row (bf16 in + out) plus w.
+//
+// qk_norm_rope: the per-head RMSNorm of q and k (ming-dit.cc:2083-2084)
+// and the interleaved-pair rotation (transpose_rope_pair_ftab_f16,
+// ming-dit.cc:1885-1895) in ONE pass, in place on the token-major
+// projection output -- the reference reads and writes q and k twice. The
+// intermediate bf16 rounding between the two steps is kept, so the result
+// is the reference's sequence of roundings. Rows stay token-major (the
+// attention reads heads at a column offset), so no transpose pass.
+#include "common.h"
+#include "kernels.h"
+
+namespace ming {
+namespace {
+
+template <int LPR, int CPL>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(
+    const uint16_t* x, long long ldx, const uint16_t* __restrict__ w,
+    uint16_t* y, long long ldy,
+    int rows, int D, float eps) {
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
+  const int sub = lane % LPR;
+  const int nch = D >> 3;
+  const bool live = row < rows;
+  const uint16_t* xr = x + (long long)(live ? row : 0) * ldx;
+  uint4 v[CPL];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = sub + LPR * i;
+    if (live && c < nch) {
+      v[i] = *reinterpret_cast<const uint4*>(xr + 8 * c);
+      const uint32_t* u = &v[i].x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = bf16_lo(u[e]), b = bf16_hi(u[e]);
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  if (!live) return;
+  uint16_t* yr = y + (long long)row * ldy;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = sub + LPR * i;
+    if (c < nch) {
+      const uint4 wv = *reinterpret_cast<const uint4*>(w + 8 * c);
+      const uint32_t* u = &v[i].x;
+      const uint32_t* wu = &wv.x;
+      uint4 o;
+      uint32_t* ou = &o.x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = __fmul_rn(__fmul_rn(bf16_lo(u[e]), inv), bf16_lo(wu[e]));
+        const float b = __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv), bf16_hi(wu[e]));
+        ou[e] = pack_bf16x2(a, b);
+      }
+      *reinterpret_cast<uint4*>(yr + 8 * c) = o;
+    }
+  }
+}
+
+// cos/sin [n][head_dim/2] from three integer positions per row: pairs
+// [0, a0/2) on axis 0, then a1/2 on axis 1, then a2/2 on axis 2;
+// freq = 1/theta^(2j/d), angle = pos*freq, both f64, stored f32
+// (build_rope_, ming-dit.cc:1443-1486).
+__global__ void rope_table_kernel(const int32_t* pt, const int32_t* ph,
+                                  const int32_t* pw, int n, int a0, int a1,
+                                  int a2, int pairs, double theta,
+                                  float* cos_t, float* sin_t) {
+  const long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (idx >= (long long)n * pairs) return;
+  const int t = (int)(idx / pairs), p = (int)(idx % pairs);
+  int axis, j, d;
+  if (p < a0 / 2) {
+    axis = 0; j = p; d = a0;
+  } else if (p < a0 / 2 + a1 / 2) {
+    axis = 1; j = p - a0 / 2; d = a1;
+  } else {
+    axis = 2; j = p - a0 / 2 - a1 / 2; d = a2;
+  }
+  const double pos = (double)(axis == 0 ? pt[t] : (axis == 1 ? ph[t] : pw[t]));
+  const double freq = 1.0 / pow(theta, (double)(2 * j) / (double)d);
+  const double ang = pos * freq;
+  cos_t[idx] = (float)cos(ang);
+  sin_t[idx] = (float)sin(ang);
+}
+
+// One 16-lane group per (row, head) of q or k; each lane owns 8 elements
+// (4 interleaved pairs) of the 128-wide head.
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    uint16_t* __restrict__ x, long long ld, int q_col, int k_col, int rows,
+    int n_heads, const uint16_t* __restrict__ wq,
+    const uint16_t* __restrict__ wk, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, float eps) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const long long hr = (long long)blockIdx.x * 16 + (tid >> 4);
+  const int sub = lane & 15;
+  const long long total = (long long)rows * 2 * n_heads;
+  const bool live = hr < total;
+  const long long hrc = live ? hr : 0;
+  const int row = (int)(hrc / (2 * n_heads));
+  const int hh = (int)(hrc % (2 * n_heads));
+  const bool isk = hh >= n_heads;
+  const int head = isk ? hh - n_heads : hh;
+  uint16_t* p = x + (long long)row * ld + (isk ? k_col : q_col) + head * 128 +
+                8 * sub;
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  const uint32_t* u = &v.x;
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = bf16_lo(u[e]), b = bf16_hi(u[e]);
+    ss = fmaf(a, a, ss);
+    ss = fmaf(b, b, ss);
+  }
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float inv = 1.0f / sqrtf(ss * (1.0f / 128.0f) + eps);
+  if (!live) return;
+  const uint4 wv = *reinterpret_cast<const uint4*>((isk ? wk : wq) + 8 * sub);
+  const uint32_t* wu = &wv.x;
+  const float4 cv = *reinterpret_cast<const float4*>(cos_t + (long long)row * 64 + 4 * sub);
+  const float4 sv = *reinterpret_cast<const float4*>(sin_t + (long long)row * 64 + 4 * sub);
+  const float cs[4] = {cv.x, cv.y, cv.z, cv.w};
+  const float sn[4] = {sv.x, sv.y, sv.z, sv.w};
+  uint4 o;
+  uint32_t* ou = &o.x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    // the norm, rounded to bf16 as the reference stores it
+    const float a = bf16_to_f32((uint16_t)f32_to_bf16_bits(
+        __fmul_rn(__fmul_rn(bf16_lo(u[e]), inv), bf16_lo(wu[e]))));
+    const float b = bf16_to_f32((uint16_t)f32_to_bf16_bits(
+        __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv), bf16_hi(wu[e]))));
+    // (a + i b)(c + i s)
+    const float re = __fsub_rn(__fmul_rn(a, cs[e]), __fmul_rn(b, sn[e]));
+    const float im = __fadd_rn(__fmul_rn(a, sn[e]), __fmul_rn(b, cs[e]));
+    ou[e] = pack_bf16x2(re, im);
+  }
+  *reinterpret_cast<uint4*>(p) = o;
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
+                          uint16_t* y, long long ldy, int rows, int D,
+                          float eps, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  const int nch = D / 8;
+  if (D % 8 != 0 || nch > 64 * 16) return hipErrorInvalidValue;
+#define MING_RMS(LPR, CPL)                                                   \
+  do {                                                                       \
+    const int rpb = 4 * (64 / (LPR));                                        \
+    hipLaunchKernelGGL((rmsnorm_kernel<LPR, CPL>), dim3((rows + rpb - 1) / rpb), \
+                       dim3(256), 0, s, x, ldx, w, y, ldy, rows, D, eps);    \
+  } while (0)
+  if (nch <= 8) MING_RMS(8, 1);
+  else if (nch <= 16) MING_RMS(16, 1);
+  else if (nch <= 32) MING_RMS(32, 1);
+  else if (nch <= 64) MING_RMS(64, 1);
+  else if (nch <= 256) MING_RMS(64, 4);
+  else if (nch <= 512) MING_RMS(64, 8);
+  else MING_RMS(64, 16);
+#undef MING_RMS
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_table(const int32_t* pt, const int32_t* ph,
+                             const int32_t* pw, int n, int a0, int a1, int a2,
+                             int head_dim, double theta, float* cos_t,
+                             float* sin_t, hipStream_t s) {
+  const int pairs = head_dim / 2;
+  const long long total = (long long)n * pairs;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((total + 255) / 256)),
+                     dim3(256), 0, s, pt, ph, pw, n, a0, a1, a2, pairs, theta,
+                     cos_t, sin_t);
+  return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
+                               int k_col, int rows, int n_heads,
+                               const uint16_t* wq, const uint16_t* wk,
+                               const float* cos_t, const float* sin_t,
+                               float eps, hipStream_t s) {
+  const long long total = (long long)rows * 2 * n_heads;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((total + 15) / 16)),
+                     dim3(256), 0, s, x, ld, q_col, k_col, rows, n_heads, wq,
+                     wk, cos_t, sin_t, eps);
+  return hipGetLastError();
+}
+
+}  // namespace ming
+
+namespace ming {
+hipError_t validate_norm_kernels() {
+  hipFuncAttributes fa;
+  const void* fns[] = {
+      reinterpret_cast<const void*>(&rmsnorm_kernel<8, 1>),
+      reinterpret_cast<const void*>(&rmsnorm_kernel<16, 1>),
+      reinterpret_cast<const void*>(&rmsnorm_kernel<32, 1>),
+      reinterpret_cast<const void*>(&rmsnorm_kernel<64, 1>),
+      reinterpret_cast<const void*>(&rmsnorm_kernel<64, 4>),
+      reinterpret_cast<const void*>(&rmsnorm_kernel<64, 8>),
+      reinterpret_cast<const void*>(&rmsnorm_kernel<64, 16>),
+      reinterpret_cast<const void*>(&rope_table_kernel),
+      reinterpret_cast<const void*>(&qk_norm_rope_kernel)};
+  for (const void* f : fns) {
+    const hipError_t e = hipFuncGetAttributes(&fa, f);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+}  // namespace ming

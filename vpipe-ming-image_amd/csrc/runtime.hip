@@ -1,0 +1,709 @@
+// Host runtime behind include/ming_dit_amd.h: contexts, resident
+// projection weights, load-time adapter binding, and the lin() dispatch
+// that builds the live LoRA stack per call.
+//
+// The live-stack rule is the reference's lora_for_ + Stack::add
+// (ming-dit.cc:3007-3022): a slot enters the stack only when it is bound on
+// the projection AND its strength is non-zero, in slot order, so an
+// all-zero call runs the base kernel alone and a lone slot computes the
+// same bits whichever slot index holds it.
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/ming_dit_amd.h"
+#include "kernels.h"
+
+namespace ming {
+hipError_t validate_qproj_kernels();
+hipError_t validate_norm_kernels();
+}  // namespace ming
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& why) {
+  g_err = why;
+  return code;
+}
+int ok() {
+  g_err.clear();
+  return MING_OK;
+}
+int hip_fail(hipError_t e, const char* what) {
+  return fail(MING_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define MING_HIP(call, what)                       \
+  do {                                             \
+    hipError_t e_ = (call);                        \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev)
+      (void)hipSetDevice(prev);
+  }
+};
+
+}  // namespace
+
+struct ming_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  ming_engagement eng{};
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  int live_weights = 0;   // a context outlives every weight made on it
+};
+
+namespace {
+
+struct LoraBind {
+  int rank = 0;     // as bound
+  int rank16 = 0;   // padded to 16 (zero rows / columns)
+  float fold = 1.0f;
+  uint16_t* A = nullptr;  // [rank16][K]
+  uint16_t* B = nullptr;  // [N_seg][rank16]
+};
+
+struct Segment {
+  int n_begin = 0;
+  int N = 0;
+  LoraBind slot[MING_MAX_LORA_SLOTS];
+};
+
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+}  // namespace
+
+struct ming_qweight {
+  ming_ctx* ctx = nullptr;
+  int N = 0, K = 0, bits = 0, group = 64;
+  uint32_t* codes_t = nullptr;
+  uint32_t* sb = nullptr;
+  uint16_t* w16 = nullptr;
+  std::vector<Segment> segs;
+  // Stacked adapter factors, rebuilt when a binding changes:
+  //   A_all [R16_all][K]     every (segment, slot) in order
+  //   B_seg[s] [N_s][R16_s]  per segment, its slots in order
+  bool stacks_dirty = true;
+  uint16_t* A_all = nullptr;
+  std::vector<uint16_t*> B_seg;
+  std::vector<int> a_row0;   // [seg*8 + slot] row in A_all
+  std::vector<int> b_col0;   // [seg*8 + slot] column in B_seg[seg]
+  std::vector<int> b_ld;     // per segment: R16 of the segment
+};
+
+namespace {
+
+void free_stacks(ming_qweight* q) {
+  if (q->A_all) (void)hipFree(q->A_all);
+  q->A_all = nullptr;
+  for (auto* b : q->B_seg)
+    if (b) (void)hipFree(b);
+  q->B_seg.clear();
+  q->stacks_dirty = true;
+}
+
+int build_stacks(ming_qweight* q) {
+  if (!q->stacks_dirty) return MING_OK;
+  hipStream_t s = q->ctx->stream;
+  // The old stacks may still be read by queued kernels.
+  MING_HIP(hipStreamSynchronize(s), "stack rebuild sync");
+  free_stacks(q);
+  const int nseg = (int)q->segs.size();
+  q->a_row0.assign(nseg * MING_MAX_LORA_SLOTS, -1);
+  q->b_col0.assign(nseg * MING_MAX_LORA_SLOTS, -1);
+  q->b_ld.assign(nseg, 0);
+  q->B_seg.assign(nseg, nullptr);
+  int rows_all = 0;
+  for (int si = 0; si < nseg; ++si) {
+    int col = 0;
+    for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
+      const LoraBind& b = q->segs[si].slot[sl];
+      if (b.rank <= 0) continue;
+      q->a_row0[si * MING_MAX_LORA_SLOTS + sl] = rows_all;
+      q->b_col0[si * MING_MAX_LORA_SLOTS + sl] = col;
+      rows_all += b.rank16;
+      col += b.rank16;
+    }
+    q->b_ld[si] = col;
+  }
+  if (rows_all == 0) {
+    q->stacks_dirty = false;
+    return MING_OK;
+  }
+  const size_t K = (size_t)q->K;
+  MING_HIP(hipMalloc(&q->A_all, (size_t)rows_all * K * 2), "A stack alloc");
+  for (int si = 0; si < nseg; ++si) {
+    const Segment& sg = q->segs[si];
+    if (q->b_ld[si] > 0)
+      MING_HIP(hipMalloc(&q->B_seg[si], (size_t)sg.N * q->b_ld[si] * 2),
+               "B stack alloc");
+    for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
+      const LoraBind& b = sg.slot[sl];
+      if (b.rank <= 0) continue;
+      const int ar = q->a_row0[si * MING_MAX_LORA_SLOTS + sl];
+      const int bc = q->b_col0[si * MING_MAX_LORA_SLOTS + sl];
+      MING_HIP(hipMemcpyAsync(q->A_all + (size_t)ar * K, b.A,
+                              (size_t)b.rank16 * K * 2,
+                              hipMemcpyDeviceToDevice, s),
+               "A stack copy");
+      MING_HIP(hipMemcpy2DAsync(q->B_seg[si] + bc, (size_t)q->b_ld[si] * 2,
+                                b.B, (size_t)b.rank16 * 2,
+                                (size_t)b.rank16 * 2, (size_t)sg.N,
+                                hipMemcpyDeviceToDevice, s),
+               "B stack copy");
+    }
+  }
+  q->stacks_dirty = false;
+  return MING_OK;
+}
+
+int ensure_scratch(ming_ctx* c, size_t bytes) {
+  if (bytes <= c->scratch_bytes) return MING_OK;
+  MING_HIP(hipStreamSynchronize(c->stream), "scratch grow sync");
+  if (c->scratch) (void)hipFree(c->scratch);
+  c->scratch = nullptr;
+  c->scratch_bytes = 0;
+  size_t want = std::max(bytes, (size_t)1 << 20);
+  if (hipMalloc(&c->scratch, want) != hipSuccess)
+    return fail(MING_ERR_ALLOC, "LoRA scratch allocation failed");
+  c->scratch_bytes = want;
+  return MING_OK;
+}
+
+// Copy `bytes` from host or device into a fresh device buffer.
+int upload(ming_ctx* c, void** dst, const void* src, size_t bytes,
+           int src_on_device) {
+  *dst = nullptr;
+  if (hipMalloc(dst, bytes) != hipSuccess)
+    return fail(MING_ERR_ALLOC, "device allocation failed");
+  const hipError_t e = hipMemcpyAsync(
+      *dst, src, bytes,
+      src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+      c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(*dst);
+    *dst = nullptr;
+    return hip_fail(e, "upload");
+  }
+  return MING_OK;
+}
+
+void destroy_qweight(ming_qweight* q) {
+  if (!q) return;
+  DeviceGuard g(q->ctx->device);
+  (void)hipStreamSynchronize(q->ctx->stream);
+  if (q->codes_t) (void)hipFree(q->codes_t);
+  if (q->sb) (void)hipFree(q->sb);
+  if (q->w16) (void)hipFree(q->w16);
+  for (auto& sg : q->segs)
+    for (auto& b : sg.slot) {
+      if (b.A) (void)hipFree(b.A);
+      if (b.B) (void)hipFree(b.B);
+    }
+  free_stacks(q);
+  q->ctx->live_weights -= 1;
+  delete q;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* ming_last_error(void) { return g_err.c_str(); }
+int ming_abi_version(void) { return MING_ABI_VERSION; }
+
+int ming_ctx_create(int device, void* hip_stream, ming_ctx** out) {
+  if (!out) return fail(MING_ERR_ARG, "ming_ctx_create: null out");
+  *out = nullptr;
+  int ndev = 0;
+  MING_HIP(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+  if (device < 0 || device >= ndev)
+    return fail(MING_ERR_ARG, "ming_ctx_create: no such device");
+  DeviceGuard g(device);
+  // Resolve and validate every kernel on this device; refuse, never degrade.
+  hipError_t e = ming::validate_qproj_kernels();
+  if (e == hipSuccess) e = ming::validate_norm_kernels();
+  if (e != hipSuccess)
+    return fail(MING_ERR_KERNEL,
+                std::string("kernel validation failed on this device (the "
+                            "library is built for gfx950): ") +
+                    hipGetErrorString(e));
+  auto* c = new (std::nothrow) ming_ctx();
+  if (!c) return fail(MING_ERR_ALLOC, "ming_ctx_create: out of memory");
+  c->device = device;
+  if (hip_stream) {
+    c->stream = (hipStream_t)hip_stream;
+  } else {
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+      delete c;
+      return fail(MING_ERR_HIP, "ming_ctx_create: stream creation failed");
+    }
+    c->own_stream = true;
+  }
+  *out = c;
+  return ok();
+}
+
+int ming_ctx_destroy(ming_ctx* c) {
+  if (!c) return ok();
+  if (c->live_weights > 0)
+    return fail(MING_ERR_STATE,
+                "ming_ctx_destroy: destroy the context's weights first");
+  DeviceGuard g(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  if (c->scratch) (void)hipFree(c->scratch);
+  if (c->own_stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+  return ok();
+}
+
+int ming_ctx_set_stream(ming_ctx* c, void* hip_stream) {
+  if (!c) return fail(MING_ERR_ARG, "null context");
+  DeviceGuard g(c->device);
+  MING_HIP(hipStreamSynchronize(c->stream), "set_stream sync");
+  if (c->own_stream) (void)hipStreamDestroy(c->stream);
+  c->own_stream = false;
+  c->stream = (hipStream_t)hip_stream;
+  return ok();
+}
+
+void* ming_ctx_stream(const ming_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+int ming_ctx_synchronize(ming_ctx* c) {
+  if (!c) return fail(MING_ERR_ARG, "null context");
+  DeviceGuard g(c->device);
+  MING_HIP(hipStreamSynchronize(c->stream), "synchronize");
+  return ok();
+}
+
+int ming_ctx_engagement(const ming_ctx* c, ming_engagement* out) {
+  if (!c || !out) return fail(MING_ERR_ARG, "null argument");
+  *out = c->eng;
+  return ok();
+}
+
+int ming_ctx_reset_engagement(ming_ctx* c) {
+  if (!c) return fail(MING_ERR_ARG, "null context");
+  c->eng = ming_engagement{};
+  return ok();
+}
+
+int ming_qweight_create(ming_ctx* c, int N, int K, int bits, int group,
+                        const uint32_t* codes, const uint16_t* scales,
+                        const uint16_t* biases, int src_on_device,
+                        ming_qweight** out) {
+  if (!c || !out || !codes || !scales || !biases)
+    return fail(MING_ERR_ARG, "ming_qweight_create: null argument");
+  *out = nullptr;
+  if (bits != 4 && bits != 8)
+    return fail(MING_ERR_SHAPE, "ming_qweight_create: bits must be 4 or 8");
+  if (group != 64)
+    return fail(MING_ERR_SHAPE, "ming_qweight_create: group must be 64");
+  if (N <= 0 || K <= 0 || K % 64 != 0 || N % 8 != 0)
+    return fail(MING_ERR_SHAPE,
+                "ming_qweight_create: need K % 64 == 0 and N % 8 == 0");
+  DeviceGuard g(c->device);
+  auto* q = new (std::nothrow) ming_qweight();
+  if (!q) return fail(MING_ERR_ALLOC, "out of memory");
+  q->ctx = c; q->N = N; q->K = K; q->bits = bits; q->group = group;
+  c->live_weights += 1;
+  q->segs.resize(1);
+  q->segs[0].N = N;
+  const size_t words = (size_t)N * K * bits / 32;
+  const size_t G = (size_t)K / 64;
+  void *dc = nullptr, *ds = nullptr, *db = nullptr;
+  int rc = upload(c, &dc, codes, words * 4, src_on_device);
+  if (rc == MING_OK) rc = upload(c, &ds, scales, (size_t)N * G * 2, src_on_device);
+  if (rc == MING_OK) rc = upload(c, &db, biases, (size_t)N * G * 2, src_on_device);
+  hipError_t e = hipSuccess;
+  if (rc == MING_OK) {
+    e = hipMalloc(&q->codes_t, words * 4);
+    if (e == hipSuccess) e = hipMalloc(&q->sb, (size_t)N * G * 4);
+    if (e == hipSuccess)
+      e = ming::launch_repack(bits, (const uint32_t*)dc, (const uint16_t*)ds,
+                              (const uint16_t*)db, N, K, q->codes_t, q->sb,
+                              c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "ming_qweight_create: repack");
+  }
+  if (dc) (void)hipFree(dc);
+  if (ds) (void)hipFree(ds);
+  if (db) (void)hipFree(db);
+  if (rc != MING_OK) {
+    destroy_qweight(q);
+    return rc;
+  }
+  *out = q;
+  return ok();
+}
+
+int ming_qweight_create_dense(ming_ctx* c, int N, int K, const uint16_t* w,
+                              int src_on_device, ming_qweight** out) {
+  if (!c || !out || !w)
+    return fail(MING_ERR_ARG, "ming_qweight_create_dense: null argument");
+  *out = nullptr;
+  if (N <= 0 || K <= 0 || K % 64 != 0 || N % 8 != 0)
+    return fail(MING_ERR_SHAPE,
+                "ming_qweight_create_dense: need K % 64 == 0 and N % 8 == 0");
+  DeviceGuard g(c->device);
+  auto* q = new (std::nothrow) ming_qweight();
+  if (!q) return fail(MING_ERR_ALLOC, "out of memory");
+  q->ctx = c; q->N = N; q->K = K; q->bits = 16;
+  c->live_weights += 1;
+  q->segs.resize(1);
+  q->segs[0].N = N;
+  void* d = nullptr;
+  int rc = upload(c, &d, w, (size_t)N * K * 2, src_on_device);
+  if (rc == MING_OK && hipStreamSynchronize(c->stream) != hipSuccess)
+    rc = fail(MING_ERR_HIP, "ming_qweight_create_dense: upload sync");
+  q->w16 = (uint16_t*)d;
+  if (rc != MING_OK) {
+    destroy_qweight(q);
+    return rc;
+  }
+  *out = q;
+  return ok();
+}
+
+int ming_qweight_concat(ming_ctx* c, int n_parts, ming_qweight* const* parts,
+                        ming_qweight** out) {
+  if (!c || !out || !parts || n_parts <= 0)
+    return fail(MING_ERR_ARG, "ming_qweight_concat: bad arguments");
+  *out = nullptr;
+  if (n_parts > ming::kMaxSeg)
+    return fail(MING_ERR_SHAPE, "ming_qweight_concat: at most 4 parts");
+  int N = 0;
+  for (int i = 0; i < n_parts; ++i) {
+    const ming_qweight* p = parts[i];
+    if (!p) return fail(MING_ERR_ARG, "ming_qweight_concat: null part");
+    if (p->ctx != c || p->K != parts[0]->K || p->bits != parts[0]->bits ||
+        p->segs.size() != 1)
+      return fail(MING_ERR_SHAPE,
+                  "ming_qweight_concat: parts must be single projections of "
+                  "one context with equal K and bits");
+    if (i + 1 < n_parts && p->N % ming::kQpBN != 0)
+      return fail(MING_ERR_SHAPE,
+                  "ming_qweight_concat: every part but the last needs "
+                  "N % 256 == 0");
+    N += p->N;
+  }
+  DeviceGuard g(c->device);
+  auto* q = new (std::nothrow) ming_qweight();
+  if (!q) return fail(MING_ERR_ALLOC, "out of memory");
+  q->ctx = c; q->N = N; q->K = parts[0]->K; q->bits = parts[0]->bits;
+  c->live_weights += 1;
+  const int K = q->K, bits = q->bits;
+  hipStream_t s = c->stream;
+  int rc = MING_OK;
+  auto chk = [&](hipError_t e, const char* what) {
+    if (rc == MING_OK && e != hipSuccess) rc = hip_fail(e, what);
+  };
+  if (bits == 16) {
+    chk(hipMalloc(&q->w16, (size_t)N * K * 2), "concat alloc");
+  } else {
+    chk(hipMalloc(&q->codes_t, (size_t)N * K * bits / 8), "concat alloc");
+    chk(hipMalloc(&q->sb, (size_t)N * (K / 64) * 4), "concat alloc");
+  }
+  q->segs.resize(n_parts);
+  int nb = 0;
+  const int KT = K / 64, wpr = bits == 4 ? 8 : 16;
+  for (int i = 0; i < n_parts && rc == MING_OK; ++i) {
+    const ming_qweight* p = parts[i];
+    Segment& sg = q->segs[i];
+    sg.n_begin = nb;
+    sg.N = p->N;
+    if (bits == 16) {
+      chk(hipMemcpyAsync(q->w16 + (size_t)nb * K, p->w16, (size_t)p->N * K * 2,
+                         hipMemcpyDeviceToDevice, s), "concat copy");
+    } else {
+      chk(hipMemcpy2DAsync(q->codes_t + (size_t)nb * wpr, (size_t)N * wpr * 4,
+                           p->codes_t, (size_t)p->N * wpr * 4,
+                           (size_t)p->N * wpr * 4, (size_t)KT,
+                           hipMemcpyDeviceToDevice, s), "concat copy");
+      chk(hipMemcpy2DAsync(q->sb + nb, (size_t)N * 4, p->sb, (size_t)p->N * 4,
+                           (size_t)p->N * 4, (size_t)KT,
+                           hipMemcpyDeviceToDevice, s), "concat copy");
+    }
+    for (int sl = 0; sl < MING_MAX_LORA_SLOTS && rc == MING_OK; ++sl) {
+      const LoraBind& b = p->segs[0].slot[sl];
+      if (b.rank <= 0) continue;
+      LoraBind& d = sg.slot[sl];
+      d.rank = b.rank; d.rank16 = b.rank16; d.fold = b.fold;
+      chk(hipMalloc(&d.A, (size_t)b.rank16 * K * 2), "concat lora alloc");
+      chk(hipMalloc(&d.B, (size_t)p->N * b.rank16 * 2), "concat lora alloc");
+      if (rc != MING_OK) break;
+      chk(hipMemcpyAsync(d.A, b.A, (size_t)b.rank16 * K * 2,
+                         hipMemcpyDeviceToDevice, s), "concat lora copy");
+      chk(hipMemcpyAsync(d.B, b.B, (size_t)p->N * b.rank16 * 2,
+                         hipMemcpyDeviceToDevice, s), "concat lora copy");
+    }
+    nb += p->N;
+  }
+  chk(hipStreamSynchronize(s), "concat sync");
+  if (rc != MING_OK) {
+    destroy_qweight(q);
+    return rc;
+  }
+  *out = q;
+  return ok();
+}
+
+int ming_qweight_destroy(ming_qweight* q) {
+  destroy_qweight(q);
+  return ok();
+}
+
+int ming_qweight_bits(const ming_qweight* q) { return q ? q->bits : 0; }
+
+int ming_qweight_shape(const ming_qweight* q, int* N, int* K, int* n_segments) {
+  if (!q) return fail(MING_ERR_ARG, "null weight");
+  if (N) *N = q->N;
+  if (K) *K = q->K;
+  if (n_segments) *n_segments = (int)q->segs.size();
+  return ok();
+}
+
+int ming_qweight_bind_lora(ming_qweight* q, int segment, int slot, int rank,
+                           const uint16_t* A, const uint16_t* B, float fold,
+                           int src_on_device) {
+  if (!q || !A || !B) return fail(MING_ERR_ARG, "bind_lora: null argument");
+  if (segment < 0 || segment >= (int)q->segs.size())
+    return fail(MING_ERR_ARG, "bind_lora: no such segment");
+  if (slot < 0 || slot >= MING_MAX_LORA_SLOTS)
+    return fail(MING_ERR_ARG, "bind_lora: slot out of range");
+  if (rank <= 0 || rank > MING_MAX_LORA_RANK)
+    return fail(MING_ERR_SHAPE, "bind_lora: rank out of range");
+  ming_ctx* c = q->ctx;
+  DeviceGuard g(c->device);
+  Segment& sg = q->segs[segment];
+  const int r16 = round_up(rank, 16);
+  const size_t K = (size_t)q->K;
+  LoraBind nb;
+  nb.rank = rank; nb.rank16 = r16; nb.fold = fold;
+  if (hipMalloc(&nb.A, (size_t)r16 * K * 2) != hipSuccess ||
+      hipMalloc(&nb.B, (size_t)sg.N * r16 * 2) != hipSuccess) {
+    if (nb.A) (void)hipFree(nb.A);
+    if (nb.B) (void)hipFree(nb.B);
+    return fail(MING_ERR_ALLOC, "bind_lora: allocation failed");
+  }
+  const hipMemcpyKind kind =
+      src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  hipError_t e = hipMemsetAsync(nb.A, 0, (size_t)r16 * K * 2, c->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(nb.B, 0, (size_t)sg.N * r16 * 2, c->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(nb.A, A, (size_t)rank * K * 2, kind, c->stream);
+  if (e == hipSuccess)
+    e = hipMemcpy2DAsync(nb.B, (size_t)r16 * 2, B, (size_t)rank * 2,
+                         (size_t)rank * 2, (size_t)sg.N, kind, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(nb.A);
+    (void)hipFree(nb.B);
+    return hip_fail(e, "bind_lora: upload");
+  }
+  LoraBind& old = sg.slot[slot];
+  if (old.A) (void)hipFree(old.A);
+  if (old.B) (void)hipFree(old.B);
+  old = nb;
+  q->stacks_dirty = true;
+  return ok();
+}
+
+int ming_qweight_unbind_lora(ming_qweight* q, int segment, int slot) {
+  if (!q) return fail(MING_ERR_ARG, "unbind_lora: null weight");
+  if (segment < 0 || segment >= (int)q->segs.size() || slot < 0 ||
+      slot >= MING_MAX_LORA_SLOTS)
+    return fail(MING_ERR_ARG, "unbind_lora: out of range");
+  DeviceGuard g(q->ctx->device);
+  (void)hipStreamSynchronize(q->ctx->stream);
+  LoraBind& b = q->segs[segment].slot[slot];
+  if (b.A) (void)hipFree(b.A);
+  if (b.B) (void)hipFree(b.B);
+  b = LoraBind{};
+  q->stacks_dirty = true;
+  return ok();
+}
+
+int ming_qweight_lora_rank(const ming_qweight* q, int segment, int slot) {
+  if (!q || segment < 0 || segment >= (int)q->segs.size() || slot < 0 ||
+      slot >= MING_MAX_LORA_SLOTS)
+    return 0;
+  return q->segs[segment].slot[slot].rank;
+}
+
+int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
+             int64_t ldx, uint16_t* y, int64_t ldy, int M,
+             const float* scales) {
+  if (!c || !qc || !x || !y) return fail(MING_ERR_ARG, "ming_lin: null argument");
+  if (qc->ctx != c) return fail(MING_ERR_ARG, "ming_lin: weight of another context");
+  ming_qweight* q = const_cast<ming_qweight*>(qc);
+  if (M < 0) return fail(MING_ERR_ARG, "ming_lin: M < 0");
+  if (ldx < q->K || ldy < q->N || ldx % 8 != 0 || ldy % 4 != 0)
+    return fail(MING_ERR_SHAPE,
+                "ming_lin: need ldx >= K, ldx % 8 == 0, ldy >= N, ldy % 4 == 0");
+  if (!aligned(x, 16) || !aligned(y, 8))
+    return fail(MING_ERR_ARG, "ming_lin: x must be 16-byte and y 8-byte aligned");
+  if (M == 0) return ok();
+  DeviceGuard g(c->device);
+
+  // The live stack, per segment, in slot order.
+  ming::QprojArgs qa{};
+  ming::LoraXaArgs xa{};
+  const int nseg = (int)q->segs.size();
+  int xa_groups = 0;   // 16-wide groups of T over all segments
+  int qp_groups = 0;
+  bool any_live = false;
+  for (int si = 0; si < nseg; ++si)
+    for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl)
+      if (q->segs[si].slot[sl].rank > 0 && scales && scales[sl] != 0.0f)
+        any_live = true;
+  if (any_live) {
+    int rc = build_stacks(q);
+    if (rc != MING_OK) return rc;
+  }
+  uint64_t lora_flops = 0;
+  int live_segs = 0;
+  for (int si = 0; si < nseg; ++si) {
+    const Segment& sg = q->segs[si];
+    ming::QprojSeg& d = qa.seg[si];
+    d.n_begin = sg.n_begin;
+    d.n_end = sg.n_begin + sg.N;
+    d.t_col0 = xa_groups * 16;
+    d.grp0 = qp_groups;
+    d.chunks = 0;
+    d.ldb = any_live ? q->b_ld[si] : 0;
+    d.B = any_live ? q->B_seg[si] : nullptr;
+    int seg_groups = 0;
+    for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
+      const LoraBind& b = sg.slot[sl];
+      if (b.rank <= 0 || !scales || scales[sl] == 0.0f) continue;
+      const int ar = q->a_row0[si * MING_MAX_LORA_SLOTS + sl];
+      const int bc = q->b_col0[si * MING_MAX_LORA_SLOTS + sl];
+      for (int gi = 0; gi < b.rank16 / 16; ++gi) {
+        if (xa_groups + seg_groups >= ming::kMaxGroups ||
+            qp_groups + seg_groups >= ming::kMaxGroups)
+          return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
+        xa.grp[xa_groups + seg_groups] = (int16_t)(ar / 16 + gi);
+        xa.coef[xa_groups + seg_groups] = b.fold * scales[sl];
+        qa.grp[qp_groups + seg_groups] = (int16_t)(bc / 16 + gi);
+        ++seg_groups;
+      }
+      lora_flops += 2ull * (uint64_t)M * (uint64_t)b.rank * (uint64_t)(q->K + sg.N);
+    }
+    if (seg_groups == 0) continue;
+    ++live_segs;
+    // pad the segment's T columns to whole 64-wide chunks with zero groups
+    const int padded = round_up(seg_groups, 4);
+    for (int gi = seg_groups; gi < padded; ++gi) {
+      if (xa_groups + gi >= ming::kMaxGroups || qp_groups + gi >= ming::kMaxGroups)
+        return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
+      xa.grp[xa_groups + gi] = -1;
+      xa.coef[xa_groups + gi] = 0.0f;
+      qa.grp[qp_groups + gi] = -1;
+    }
+    d.chunks = padded / 4;
+    xa_groups += padded;
+    qp_groups += padded;
+  }
+  const int t_cols = xa_groups * 16;
+  uint16_t* T = nullptr;
+  if (t_cols > 0) {
+    int rc = ensure_scratch(c, (size_t)M * t_cols * 2);
+    if (rc != MING_OK) return rc;
+    T = (uint16_t*)c->scratch;
+    xa.x = x; xa.ldx = ldx; xa.A = q->A_all; xa.K = q->K; xa.M = M;
+    xa.n_cols = t_cols; xa.t = T; xa.ldt = t_cols;
+    MING_HIP(ming::launch_lora_xa(xa, c->stream), "lora_xa launch");
+    c->eng.lora_xa += 1;
+  }
+  qa.x = x; qa.ldx = ldx; qa.codes = q->codes_t; qa.sb = q->sb; qa.w16 = q->w16;
+  qa.y = y; qa.ldy = ldy; qa.M = M; qa.N = q->N; qa.K = q->K;
+  qa.t = T; qa.ldt = t_cols > 0 ? t_cols : 0; qa.nseg = nseg;
+  MING_HIP(ming::launch_qproj(q->bits, qa, c->stream), "qproj launch");
+  if (q->bits == 4) c->eng.gemm_q4 += 1;
+  else if (q->bits == 8) c->eng.gemm_q8 += 1;
+  else c->eng.gemm_dense += 1;
+  c->eng.lora_proj += live_segs;
+  c->eng.gemm_flops += 2ull * (uint64_t)M * (uint64_t)q->N * (uint64_t)q->K + lora_flops;
+  return ok();
+}
+
+int ming_rmsnorm(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                 uint16_t* y, int64_t ldy, int rows, int D, float eps) {
+  if (!c || !x || !w || !y) return fail(MING_ERR_ARG, "ming_rmsnorm: null argument");
+  if (rows < 0 || D <= 0 || D % 8 != 0 || D > 8192)
+    return fail(MING_ERR_SHAPE, "ming_rmsnorm: need D % 8 == 0 and D <= 8192");
+  if (ldx < D || ldy < D || ldx % 8 != 0 || ldy % 8 != 0)
+    return fail(MING_ERR_SHAPE, "ming_rmsnorm: bad row strides");
+  if (!aligned(x, 16) || !aligned(y, 16) || !aligned(w, 16))
+    return fail(MING_ERR_ARG, "ming_rmsnorm: pointers must be 16-byte aligned");
+  if (rows == 0) return ok();
+  DeviceGuard g(c->device);
+  MING_HIP(ming::launch_rmsnorm(x, ldx, w, y, ldy, rows, D, eps, c->stream),
+           "rmsnorm launch");
+  c->eng.rmsnorm += 1;
+  return ok();
+}
+
+int ming_rope_table(ming_ctx* c, const int32_t* pos_t, const int32_t* pos_h,
+                    const int32_t* pos_w, int n, const int* axes, int head_dim,
+                    double theta, float* cos_out, float* sin_out) {
+  if (!c || !pos_t || !pos_h || !pos_w || !axes || !cos_out || !sin_out)
+    return fail(MING_ERR_ARG, "ming_rope_table: null argument");
+  if (n < 0 || head_dim <= 0 || head_dim % 2 != 0 || axes[0] < 0 ||
+      axes[1] < 0 || axes[2] < 0 || axes[0] % 2 || axes[1] % 2 || axes[2] % 2 ||
+      axes[0] + axes[1] + axes[2] != head_dim)
+    return fail(MING_ERR_SHAPE, "ming_rope_table: axes must be even and sum to head_dim");
+  if (n == 0) return ok();
+  DeviceGuard g(c->device);
+  MING_HIP(ming::launch_rope_table(pos_t, pos_h, pos_w, n, axes[0], axes[1],
+                                   axes[2], head_dim, theta, cos_out, sin_out,
+                                   c->stream),
+           "rope_table launch");
+  c->eng.rope_table += 1;
+  return ok();
+}
+
+int ming_qk_norm_rope(ming_ctx* c, uint16_t* x, int64_t ld, int q_col, int k_col,
+                      int rows, int n_heads, int head_dim, const uint16_t* wq,
+                      const uint16_t* wk, const float* cos_t, const float* sin_t,
+                      float eps) {
+  if (!c || !x || !wq || !wk || !cos_t || !sin_t)
+    return fail(MING_ERR_ARG, "ming_qk_norm_rope: null argument");
+  if (head_dim != 128)
+    return fail(MING_ERR_SHAPE, "ming_qk_norm_rope: head_dim must be 128");
+  if (rows < 0 || n_heads <= 0 || q_col < 0 || k_col < 0 || q_col % 8 ||
+      k_col % 8 || ld % 8 || q_col + n_heads * 128 > ld ||
+      k_col + n_heads * 128 > ld)
+    return fail(MING_ERR_SHAPE, "ming_qk_norm_rope: bad columns or stride");
+  if (!aligned(x, 16) || !aligned(wq, 16) || !aligned(wk, 16) ||
+      !aligned(cos_t, 16) || !aligned(sin_t, 16))
+    return fail(MING_ERR_ARG, "ming_qk_norm_rope: pointers must be 16-byte aligned");
+  if (rows == 0) return ok();
+  DeviceGuard g(c->device);
+  MING_HIP(ming::launch_qk_norm_rope(x, ld, q_col, k_col, rows, n_heads, wq, wk,
+                                     cos_t, sin_t, eps, c->stream),
+           "qk_norm_rope launch");
+  c->eng.qk_norm_rope += 1;
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,250 @@
+"""Python face of libming_dit_amd.so (the C-ABI in include/ming_dit_amd.h).
+
+Thin ctypes plumbing for tests, bench.py and the graft entry: device
+memory is whatever the caller owns (torch tensors here, passed by
+data_ptr()). Every entry point raises MingError with the library's own
+reason on a non-zero status. There is no fallback: if the library is not
+built, importing it raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import weakref
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libming_dit_amd.so")
+HEADER = os.path.join(os.path.dirname(_HERE), "include", "ming_dit_amd.h")
+MAX_SLOTS = 8
+
+_lib = None
+
+
+class MingError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class Engagement(C.Structure):
+    _fields_ = [("gemm_q4", C.c_int64), ("gemm_q8", C.c_int64),
+                ("gemm_dense", C.c_int64), ("lora_proj", C.c_int64),
+                ("lora_xa", C.c_int64), ("rmsnorm", C.c_int64),
+                ("qk_norm_rope", C.c_int64), ("rope_table", C.c_int64),
+                ("attention", C.c_int64), ("elementwise", C.c_int64),
+                ("gemm_flops", C.c_uint64)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+def lib():
+    """Load the built library (raises if it is not there)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+    L = C.CDLL(LIB_PATH)
+    vp, i32, i64, f32 = C.c_void_p, C.c_int, C.c_int64, C.c_float
+    sig = {
+        "ming_last_error": ([], C.c_char_p),
+        "ming_abi_version": ([], i32),
+        "ming_ctx_create": ([i32, vp, C.POINTER(vp)], i32),
+        "ming_ctx_destroy": ([vp], i32),
+        "ming_ctx_set_stream": ([vp, vp], i32),
+        "ming_ctx_stream": ([vp], vp),
+        "ming_ctx_synchronize": ([vp], i32),
+        "ming_ctx_engagement": ([vp, C.POINTER(Engagement)], i32),
+        "ming_ctx_reset_engagement": ([vp], i32),
+        "ming_qweight_create": ([vp, i32, i32, i32, i32, vp, vp, vp, i32,
+                                 C.POINTER(vp)], i32),
+        "ming_qweight_create_dense": ([vp, i32, i32, vp, i32, C.POINTER(vp)],
+                                      i32),
+        "ming_qweight_concat": ([vp, i32, C.POINTER(vp), C.POINTER(vp)], i32),
+        "ming_qweight_destroy": ([vp], i32),
+        "ming_qweight_bits": ([vp], i32),
+        "ming_qweight_shape": ([vp, C.POINTER(i32), C.POINTER(i32),
+                                C.POINTER(i32)], i32),
+        "ming_qweight_bind_lora": ([vp, i32, i32, i32, vp, vp, f32, i32], i32),
+        "ming_qweight_unbind_lora": ([vp, i32, i32], i32),
+        "ming_qweight_lora_rank": ([vp, i32, i32], i32),
+        "ming_lin": ([vp, vp, vp, i64, vp, i64, i32, C.POINTER(f32)], i32),
+        "ming_rmsnorm": ([vp, vp, i64, vp, vp, i64, i32, i32, f32], i32),
+        "ming_rope_table": ([vp, vp, vp, vp, i32, C.POINTER(i32), i32,
+                             C.c_double, vp, vp], i32),
+        "ming_qk_norm_rope": ([vp, vp, i64, i32, i32, i32, i32, i32, vp, vp,
+                               vp, vp, f32], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc != 0:
+        msg = lib().ming_last_error().decode(errors="replace")
+        raise MingError(rc, msg)
+
+
+def _ptr(t) -> int:
+    """Device (or host numpy) pointer of a tensor / array / int."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+def _scales(scales):
+    arr = (C.c_float * MAX_SLOTS)()
+    if scales is not None:
+        for i, s in enumerate(list(scales)[:MAX_SLOTS]):
+            arr[i] = float(s)
+    return arr
+
+
+class Ctx:
+    """A device + stream context (ming_ctx)."""
+
+    def __init__(self, device: int = 0, stream: int | None = None):
+        h = C.c_void_p()
+        _check(lib().ming_ctx_create(device, stream, C.byref(h)))
+        self.h = h
+        self._weights = weakref.WeakSet()
+
+    def close(self):
+        """Destroys the context's live weights first (the C-ABI refuses a
+        context that still has weights)."""
+        if self.h:
+            for w in list(self._weights):
+                w.close()
+            _check(lib().ming_ctx_destroy(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream: int | None):
+        _check(lib().ming_ctx_set_stream(self.h, stream))
+
+    def synchronize(self):
+        _check(lib().ming_ctx_synchronize(self.h))
+
+    def engagement(self) -> dict:
+        e = Engagement()
+        _check(lib().ming_ctx_engagement(self.h, C.byref(e)))
+        return e.as_dict()
+
+    def reset_engagement(self):
+        _check(lib().ming_ctx_reset_engagement(self.h))
+
+    # ---- ops ----
+    def lin(self, qw: "QWeight", x, y, M: int, scales=None, ldx=None,
+            ldy=None):
+        ldx = qw.K if ldx is None else ldx
+        ldy = qw.N if ldy is None else ldy
+        _check(lib().ming_lin(self.h, qw.h, _ptr(x), ldx, _ptr(y), ldy, M,
+                              _scales(scales)))
+
+    def rmsnorm(self, x, w, y, rows: int, D: int, eps: float = 1e-5,
+                ldx=None, ldy=None):
+        _check(lib().ming_rmsnorm(self.h, _ptr(x), D if ldx is None else ldx,
+                                  _ptr(w), _ptr(y), D if ldy is None else ldy,
+                                  rows, D, eps))
+
+    def rope_table(self, pos_t, pos_h, pos_w, n: int, cos_out, sin_out,
+                   axes=(32, 48, 48), head_dim: int = 128,
+                   theta: float = 256.0):
+        ax = (C.c_int * 3)(*axes)
+        _check(lib().ming_rope_table(self.h, _ptr(pos_t), _ptr(pos_h),
+                                     _ptr(pos_w), n, ax, head_dim, theta,
+                                     _ptr(cos_out), _ptr(sin_out)))
+
+    def qk_norm_rope(self, x, ld: int, q_col: int, k_col: int, rows: int,
+                     n_heads: int, wq, wk, cos_t, sin_t, eps: float = 1e-5,
+                     head_dim: int = 128):
+        _check(lib().ming_qk_norm_rope(self.h, _ptr(x), ld, q_col, k_col, rows,
+                                       n_heads, head_dim, _ptr(wq), _ptr(wk),
+                                       _ptr(cos_t), _ptr(sin_t), eps))
+
+
+class QWeight:
+    """A resident projection weight (ming_qweight)."""
+
+    def __init__(self, ctx: Ctx, h):
+        self.ctx = ctx
+        self.h = h
+        ctx._weights.add(self)
+        N, K, S = C.c_int(), C.c_int(), C.c_int()
+        _check(lib().ming_qweight_shape(h, C.byref(N), C.byref(K),
+                                        C.byref(S)))
+        self.N, self.K, self.n_segments = N.value, K.value, S.value
+        self.bits = lib().ming_qweight_bits(h)
+
+    @classmethod
+    def quantized(cls, ctx: Ctx, codes, scales, biases, bits: int,
+                  group: int = 64, on_device: bool = False):
+        N = int(codes.shape[0])
+        K = int(codes.shape[1]) * 32 // bits
+        h = C.c_void_p()
+        _check(lib().ming_qweight_create(ctx.h, N, K, bits, group,
+                                         _ptr(codes), _ptr(scales),
+                                         _ptr(biases), int(on_device),
+                                         C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def dense(cls, ctx: Ctx, w, on_device: bool = False):
+        N, K = int(w.shape[0]), int(w.shape[1])
+        h = C.c_void_p()
+        _check(lib().ming_qweight_create_dense(ctx.h, N, K, _ptr(w),
+                                               int(on_device), C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def concat(cls, ctx: Ctx, parts):
+        arr = (C.c_void_p * len(parts))(*[p.h.value for p in parts])
+        h = C.c_void_p()
+        _check(lib().ming_qweight_concat(ctx.h, len(parts), arr, C.byref(h)))
+        return cls(ctx, h)
+
+    def bind_lora(self, slot: int, A, B, fold: float = 1.0, segment: int = 0,
+                  on_device: bool = False):
+        rank = int(A.shape[0])
+        _check(lib().ming_qweight_bind_lora(self.h, segment, slot, rank,
+                                            _ptr(A), _ptr(B), fold,
+                                            int(on_device)))
+
+    def unbind_lora(self, slot: int, segment: int = 0):
+        _check(lib().ming_qweight_unbind_lora(self.h, segment, slot))
+
+    def lora_rank(self, slot: int, segment: int = 0) -> int:
+        return lib().ming_qweight_lora_rank(self.h, segment, slot)
+
+    def close(self):
+        if self.h:
+            lib().ming_qweight_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def header_symbols(path: str = HEADER):
+    """Every function the public header declares."""
+    import re
+    txt = open(path).read()
+    return sorted(set(re.findall(r"\b(ming_[a-z0-9_]+)\s*\(", txt)))
