@@ -64,6 +64,20 @@ typedef struct ming_engagement {
   uint64_t gemm_flops;  /* 2*M*N*K + sum_live 2*M*r*(K+N) per projection */
 } ming_engagement;
 
+/* Per-launch kernel timing (HIP events around each launch, on the
+ * context's stream), summed per kernel family -- the reference's profile
+ * buckets (ming-dit.cc:1689-1717) without its commit+wait per mark. flops
+ * and bytes are the ALGORITHMIC work of the timed launches: GEMM flops
+ * 2*M*N*K (+ the LoRA's 2*M*r*K in lora_xa and 2*M*r*N in the tail),
+ * bytes read + written once. */
+typedef struct ming_profile_bucket {
+  char name[24];
+  int64_t launches;
+  double ms;
+  double flops;
+  double bytes;
+} ming_profile_bucket;
+
 /* Last error of the CALLING thread; "" when the last call succeeded. */
 const char* ming_last_error(void);
 int ming_abi_version(void);
@@ -81,6 +95,11 @@ void* ming_ctx_stream(const ming_ctx* ctx);
 int ming_ctx_synchronize(ming_ctx* ctx);
 int ming_ctx_engagement(const ming_ctx* ctx, ming_engagement* out);
 int ming_ctx_reset_engagement(ming_ctx* ctx);
+/* Profiling on/off; collect waits for the stream, fills up to `max`
+ * non-empty buckets and clears the records. */
+int ming_ctx_set_profiling(ming_ctx* ctx, int on);
+int ming_ctx_profile_collect(ming_ctx* ctx, ming_profile_bucket* out, int max,
+                             int* n_out);
 
 /* ---- projection weights (the quant pack) ------------------------------------
  * A quantized projection in the reference's pack layout (load_qw_,
@@ -155,6 +174,47 @@ int ming_qk_norm_rope(ming_ctx* ctx, uint16_t* x, int64_t ld, int q_col,
                       int k_col, int rows, int n_heads, int head_dim,
                       const uint16_t* wq, const uint16_t* wk,
                       const float* cos_t, const float* sin_t, float eps);
+
+/* ---- block glue (ming_ops.metal; ming-dit.cc:1772-1884) -----------------------
+ * All bf16, token-major, element strides; widths and strides multiples of
+ * 8 and pointers 16-byte aligned where noted. */
+/* out = bf16(silu(g) * u), silu(g) = g / (1 + exp(-g)): swiglu_v4_f16. */
+int ming_swiglu(ming_ctx* ctx, const uint16_t* g, int64_t ldg,
+                const uint16_t* u, int64_t ldu, uint16_t* out, int64_t ldo,
+                int rows, int n);
+/* h = bf16(h + tanh(gate[n]) * sub): gated_residual_tanh_v4_f16. */
+int ming_gated_residual(ming_ctx* ctx, uint16_t* h, int64_t ldh,
+                        const uint16_t* gate, const uint16_t* sub,
+                        int64_t lds, int rows, int n);
+/* h = bf16(h + sub): residual_add_v4_f16 (the context refiner). */
+int ming_residual_add(ming_ctx* ctx, uint16_t* h, int64_t ldh,
+                      const uint16_t* sub, int64_t lds, int rows, int n);
+/* y = bf16(x * (1 + scale[n])): the model's modulation with its zero
+ * shift; over one row it folds the block's scale into a norm gain
+ * (fill_mod, ming-dit.cc:2266-2273). */
+int ming_modulate(ming_ctx* ctx, const uint16_t* x, int64_t ldx,
+                  const uint16_t* scale, uint16_t* y, int64_t ldy, int rows,
+                  int n);
+/* y = bf16(y + bias[n]), then silu when `silu` != 0 (bias, silu). */
+int ming_bias_act(ming_ctx* ctx, uint16_t* y, int64_t ldy,
+                  const uint16_t* bias, int rows, int n, int silu);
+/* y = bf16(silu(x)) over n elements. */
+int ming_silu(ming_ctx* ctx, const uint16_t* x, uint16_t* y, int n);
+/* The final layer's LayerNorm (no affine) then * (1 + scale[n])
+ * (ming-dit.cc:2553-2563, eps 1e-6 there). */
+int ming_ln_modulate(ming_ctx* ctx, const uint16_t* x, int64_t ldx,
+                     const uint16_t* scale, uint16_t* y, int64_t ldy, int rows,
+                     int D, float eps);
+
+/* ---- the pack quantizer (ming-quant-family.cc:31-59's recipe target) -----------
+ * Device f32 w [N, K] -> the pack layout ming_qweight_create reads: bits 8
+ * symmetric (s = bf16(max|w|/127), code = clamp(rint(w/s), -127, 127) +
+ * 128, bias = -128 s) or bits 4 affine (s = bf16((max-min)/15),
+ * b = bf16(min), code = clamp(rint((w-b)/s), 0, 15)), group 64, codes
+ * LSB-first. */
+int ming_quantize_pack(ming_ctx* ctx, const float* w, int N, int K, int bits,
+                       int group, uint32_t* codes, uint16_t* scales,
+                       uint16_t* biases);
 
 #ifdef __cplusplus
 }

@@ -662,6 +662,49 @@ or_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, size_t n)
   }
 }
 
+/* y = bf16(y + b[n]), then bf16(silu(.)) when silu != 0: the bias and
+ * silu dispatches of ming-dit.cc:1773-1794 (timestep MLP, adaLN). */
+OR_EXPORT void
+or_bias_act(uint16_t* y, int ldy, const uint16_t* b, int rows, int N,
+            int silu)
+{
+  for (int r = 0; r < rows; ++r) {
+    for (int n = 0; n < N; ++n) {
+      float v = or_bf16_to_f32(or_bf16_rne(
+          or_bf16_to_f32(y[(size_t)r * ldy + n]) + or_bf16_to_f32(b[n])));
+      if (silu) { v = v / (1.0f + expf(-v)); }
+      y[(size_t)r * ldy + n] = or_bf16_rne(v);
+    }
+  }
+}
+
+/* The final layer: LayerNorm without affine (eps 1e-6 there), rounded to
+ * bf16, then * (1 + scale[n]) (ming-dit.cc:2553-2563; docs/MING-IMAGE.md
+ * 2.2 "Final layer"). Mean and variance in f64 here. */
+OR_EXPORT void
+or_ln_modulate(const uint16_t* x, int ldx, const uint16_t* scale, uint16_t* y,
+               int ldy, int rows, int D, float eps)
+{
+  for (int r = 0; r < rows; ++r) {
+    const uint16_t* xr = x + (size_t)r * ldx;
+    double s = 0.0;
+    for (int d = 0; d < D; ++d) { s += (double)or_bf16_to_f32(xr[d]); }
+    const float mean = (float)(s / D);
+    double v = 0.0;
+    for (int d = 0; d < D; ++d) {
+      const double t = (double)(or_bf16_to_f32(xr[d]) - mean);
+      v += t * t;
+    }
+    const float inv = 1.0f / sqrtf((float)(v / D) + eps);
+    for (int d = 0; d < D; ++d) {
+      const float nrm = or_bf16_to_f32(
+          or_bf16_rne((or_bf16_to_f32(xr[d]) - mean) * inv));
+      y[(size_t)r * ldy + d] =
+          or_bf16_rne(nrm * (1.0f + or_bf16_to_f32(scale[d])));
+    }
+  }
+}
+
 /* Non-causal, maskless softmax(q k^T * scale) v per head, f64 internally,
  * bf16 out: the dense attention run_attn dispatches
  * (ming-dit.cc:1905-2039). q/k/v/o are token-major [rows][ld] with head h

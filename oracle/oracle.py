@@ -85,6 +85,10 @@ def lib():
     L.or_gated_residual.argtypes = [_u16p, C.c_int, _u16p, _u16p, C.c_int,
                                     C.c_int, C.c_int]
     L.or_swiglu.argtypes = [_u16p, _u16p, _u16p, C.c_size_t]
+    L.or_bias_act.argtypes = [_u16p, C.c_int, _u16p, C.c_int, C.c_int,
+                              C.c_int]
+    L.or_ln_modulate.argtypes = [_u16p, C.c_int, _u16p, _u16p, C.c_int,
+                                 C.c_int, C.c_int, C.c_float]
     L.or_attention.argtypes = [_u16p, C.c_int, _u16p, C.c_int, _u16p, C.c_int,
                                _u16p, C.c_int, C.c_int, C.c_int, C.c_int,
                                C.c_float]
@@ -300,6 +304,23 @@ def swiglu(g_bf16, u_bf16) -> np.ndarray:
                                                          np.uint16).reshape(-1),
                     out.reshape(-1), g.size)
     return out
+
+
+def bias_act(y_bf16, b_bf16, silu=False) -> np.ndarray:
+    y = np.array(y_bf16, np.uint16, copy=True, order="C")
+    rows, N = y.shape
+    lib().or_bias_act(y, N, np.ascontiguousarray(b_bf16, np.uint16), rows, N,
+                      int(silu))
+    return y
+
+
+def ln_modulate(x_bf16, scale_bf16, eps=1e-6) -> np.ndarray:
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    rows, D = x.shape
+    y = np.empty_like(x)
+    lib().or_ln_modulate(x, D, np.ascontiguousarray(scale_bf16, np.uint16), y,
+                         D, rows, D, eps)
+    return y
 
 
 def attention(q, k, v, n_heads, head_dim, scale=None) -> np.ndarray:

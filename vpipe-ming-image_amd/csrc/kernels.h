@@ -90,4 +90,29 @@ hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
                                const float* cos_t, const float* sin_t,
                                float eps, hipStream_t s);
 
+// ---- block glue and the pack quantizer (elementwise.hip) ----------------------
+hipError_t launch_swiglu(const uint16_t* g, long long ldg, const uint16_t* u,
+                         long long ldu, uint16_t* out, long long ldo, int rows,
+                         int n, hipStream_t s);
+hipError_t launch_residual(uint16_t* h, long long ldh, const uint16_t* gate,
+                           const uint16_t* sub, long long lds, int rows, int n,
+                           int gated, hipStream_t s);
+hipError_t launch_modulate(const uint16_t* x, long long ldx,
+                           const uint16_t* scale, uint16_t* y, long long ldy,
+                           int rows, int n, hipStream_t s);
+hipError_t launch_bias_act(uint16_t* y, long long ldy, const uint16_t* b,
+                           uint16_t* out2, int rows, int n, int mode,
+                           hipStream_t s);
+hipError_t launch_ln_modulate(const uint16_t* x, long long ldx,
+                              const uint16_t* scale, uint16_t* y,
+                              long long ldy, int rows, int D, float eps,
+                              hipStream_t s);
+hipError_t launch_quantize(const float* w, int N, int K, int bits,
+                           uint32_t* codes, uint16_t* scales, uint16_t* biases,
+                           hipStream_t s);
+
+hipError_t validate_qproj_kernels();
+hipError_t validate_norm_kernels();
+hipError_t validate_elementwise_kernels();
+
 }  // namespace ming

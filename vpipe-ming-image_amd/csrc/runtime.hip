@@ -17,11 +17,6 @@
 #include "../../include/ming_dit_amd.h"
 #include "kernels.h"
 
-namespace ming {
-hipError_t validate_qproj_kernels();
-hipError_t validate_norm_kernels();
-}  // namespace ming
-
 namespace {
 
 thread_local std::string g_err;
@@ -67,9 +62,55 @@ struct ming_ctx {
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
   int live_weights = 0;   // a context outlives every weight made on it
+  // Per-launch HIP-event timing (ming_ctx_set_profiling), by bucket.
+  bool profiling = false;
+  struct Rec { int bucket; hipEvent_t a, b; double flops, bytes; };
+  std::vector<Rec> recs;
+  std::vector<hipEvent_t> pool;
 };
 
 namespace {
+
+// Profile buckets: one per kernel family (the reference's per-category
+// marks, ming-dit.cc:1689-1717, as HIP events around each launch).
+enum Bucket {
+  kBQ4, kBQ8, kBDense, kBXa, kBRms, kBQkRope, kBRopeTab, kBSwiglu, kBResid,
+  kBModulate, kBBias, kBLn, kBQuant, kBAttn, kBCount
+};
+const char* const kBucketName[kBCount] = {
+    "qproj.w4", "qproj.w8", "qproj.dense", "lora_xa", "rmsnorm",
+    "qk_norm_rope", "rope_table", "swiglu", "residual", "modulate",
+    "bias_act", "ln_modulate", "quantize", "attention"};
+
+hipEvent_t take_event(ming_ctx* c) {
+  if (!c->pool.empty()) {
+    hipEvent_t e = c->pool.back();
+    c->pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Runs `launch` (returning hipError_t), bracketed by events when profiling.
+template <class F>
+hipError_t profiled(ming_ctx* c, int bucket, double flops, double bytes,
+                    F&& launch) {
+  if (!c->profiling) return launch();
+  hipEvent_t a = take_event(c), b = take_event(c);
+  if (!a || !b) return hipErrorOutOfMemory;
+  hipError_t e = hipEventRecord(a, c->stream);
+  if (e == hipSuccess) e = launch();
+  if (e == hipSuccess) e = hipEventRecord(b, c->stream);
+  if (e != hipSuccess) {
+    c->pool.push_back(a);
+    c->pool.push_back(b);
+    return e;
+  }
+  c->recs.push_back({bucket, a, b, flops, bytes});
+  return hipSuccess;
+}
 
 struct LoraBind {
   int rank = 0;     // as bound
@@ -241,6 +282,7 @@ int ming_ctx_create(int device, void* hip_stream, ming_ctx** out) {
   // Resolve and validate every kernel on this device; refuse, never degrade.
   hipError_t e = ming::validate_qproj_kernels();
   if (e == hipSuccess) e = ming::validate_norm_kernels();
+  if (e == hipSuccess) e = ming::validate_elementwise_kernels();
   if (e != hipSuccess)
     return fail(MING_ERR_KERNEL,
                 std::string("kernel validation failed on this device (the "
@@ -270,6 +312,11 @@ int ming_ctx_destroy(ming_ctx* c) {
   DeviceGuard g(c->device);
   (void)hipStreamSynchronize(c->stream);
   if (c->scratch) (void)hipFree(c->scratch);
+  for (auto& rec : c->recs) {
+    (void)hipEventDestroy(rec.a);
+    (void)hipEventDestroy(rec.b);
+  }
+  for (auto e : c->pool) (void)hipEventDestroy(e);
   if (c->own_stream) (void)hipStreamDestroy(c->stream);
   delete c;
   return ok();
@@ -631,13 +678,38 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
     T = (uint16_t*)c->scratch;
     xa.x = x; xa.ldx = ldx; xa.A = q->A_all; xa.K = q->K; xa.M = M;
     xa.n_cols = t_cols; xa.t = T; xa.ldt = t_cols;
-    MING_HIP(ming::launch_lora_xa(xa, c->stream), "lora_xa launch");
+    double xa_flops = 0.0;
+    for (int si = 0; si < nseg; ++si)
+      for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
+        const LoraBind& b = q->segs[si].slot[sl];
+        if (b.rank > 0 && scales && scales[sl] != 0.0f)
+          xa_flops += 2.0 * M * b.rank * (double)q->K;
+      }
+    MING_HIP(profiled(c, kBXa, xa_flops,
+                      2.0 * M * q->K + 2.0 * t_cols * (double)q->K + 2.0 * M * t_cols,
+                      [&] { return ming::launch_lora_xa(xa, c->stream); }),
+             "lora_xa launch");
     c->eng.lora_xa += 1;
   }
   qa.x = x; qa.ldx = ldx; qa.codes = q->codes_t; qa.sb = q->sb; qa.w16 = q->w16;
   qa.y = y; qa.ldy = ldy; qa.M = M; qa.N = q->N; qa.K = q->K;
   qa.t = T; qa.ldt = t_cols > 0 ? t_cols : 0; qa.nseg = nseg;
-  MING_HIP(ming::launch_qproj(q->bits, qa, c->stream), "qproj launch");
+  const double base_flops = 2.0 * M * (double)q->N * q->K;
+  double tail_flops = 0.0;
+  for (int si = 0; si < nseg; ++si)
+    for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
+      const LoraBind& b = q->segs[si].slot[sl];
+      if (b.rank > 0 && scales && scales[sl] != 0.0f)
+        tail_flops += 2.0 * M * b.rank * (double)q->segs[si].N;
+    }
+  const double wbytes = q->bits == 16
+                            ? 2.0 * q->N * q->K
+                            : (double)q->N * q->K * q->bits / 8 + 4.0 * q->N * (q->K / 64);
+  const int bk = q->bits == 4 ? kBQ4 : (q->bits == 8 ? kBQ8 : kBDense);
+  MING_HIP(profiled(c, bk, base_flops + tail_flops,
+                    2.0 * M * q->K + wbytes + 2.0 * M * q->N,
+                    [&] { return ming::launch_qproj(q->bits, qa, c->stream); }),
+           "qproj launch");
   if (q->bits == 4) c->eng.gemm_q4 += 1;
   else if (q->bits == 8) c->eng.gemm_q8 += 1;
   else c->eng.gemm_dense += 1;
@@ -657,7 +729,9 @@ int ming_rmsnorm(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* w,
     return fail(MING_ERR_ARG, "ming_rmsnorm: pointers must be 16-byte aligned");
   if (rows == 0) return ok();
   DeviceGuard g(c->device);
-  MING_HIP(ming::launch_rmsnorm(x, ldx, w, y, ldy, rows, D, eps, c->stream),
+  MING_HIP(profiled(c, kBRms, 0.0, 4.0 * rows * D + 2.0 * D,
+                    [&] { return ming::launch_rmsnorm(x, ldx, w, y, ldy, rows, D,
+                                                      eps, c->stream); }),
            "rmsnorm launch");
   c->eng.rmsnorm += 1;
   return ok();
@@ -674,9 +748,11 @@ int ming_rope_table(ming_ctx* c, const int32_t* pos_t, const int32_t* pos_h,
     return fail(MING_ERR_SHAPE, "ming_rope_table: axes must be even and sum to head_dim");
   if (n == 0) return ok();
   DeviceGuard g(c->device);
-  MING_HIP(ming::launch_rope_table(pos_t, pos_h, pos_w, n, axes[0], axes[1],
-                                   axes[2], head_dim, theta, cos_out, sin_out,
-                                   c->stream),
+  MING_HIP(profiled(c, kBRopeTab, 0.0, 12.0 * n + 4.0 * n * head_dim,
+                    [&] { return ming::launch_rope_table(pos_t, pos_h, pos_w, n,
+                                                         axes[0], axes[1], axes[2],
+                                                         head_dim, theta, cos_out,
+                                                         sin_out, c->stream); }),
            "rope_table launch");
   c->eng.rope_table += 1;
   return ok();
@@ -699,10 +775,184 @@ int ming_qk_norm_rope(ming_ctx* c, uint16_t* x, int64_t ld, int q_col, int k_col
     return fail(MING_ERR_ARG, "ming_qk_norm_rope: pointers must be 16-byte aligned");
   if (rows == 0) return ok();
   DeviceGuard g(c->device);
-  MING_HIP(ming::launch_qk_norm_rope(x, ld, q_col, k_col, rows, n_heads, wq, wk,
-                                     cos_t, sin_t, eps, c->stream),
+  MING_HIP(profiled(c, kBQkRope, 0.0, 8.0 * rows * n_heads * 128 + 512.0,
+                    [&] { return ming::launch_qk_norm_rope(x, ld, q_col, k_col, rows,
+                                                           n_heads, wq, wk, cos_t,
+                                                           sin_t, eps, c->stream); }),
            "qk_norm_rope launch");
   c->eng.qk_norm_rope += 1;
+  return ok();
+}
+
+
+int ming_ctx_set_profiling(ming_ctx* c, int on) {
+  if (!c) return fail(MING_ERR_ARG, "null context");
+  c->profiling = on != 0;
+  return ok();
+}
+
+int ming_ctx_profile_collect(ming_ctx* c, ming_profile_bucket* out, int max,
+                             int* n_out) {
+  if (!c || (!out && max > 0)) return fail(MING_ERR_ARG, "null argument");
+  DeviceGuard g(c->device);
+  MING_HIP(hipStreamSynchronize(c->stream), "profile sync");
+  ming_profile_bucket acc[kBCount];
+  std::memset(acc, 0, sizeof(acc));
+  for (auto& rec : c->recs) {
+    float ms = 0.0f;
+    const hipError_t e = hipEventElapsedTime(&ms, rec.a, rec.b);
+    if (e == hipSuccess) {
+      acc[rec.bucket].launches += 1;
+      acc[rec.bucket].ms += ms;
+      acc[rec.bucket].flops += rec.flops;
+      acc[rec.bucket].bytes += rec.bytes;
+    }
+    c->pool.push_back(rec.a);
+    c->pool.push_back(rec.b);
+  }
+  c->recs.clear();
+  int n = 0;
+  for (int b = 0; b < kBCount; ++b) {
+    if (acc[b].launches == 0) continue;
+    if (n < max) {
+      out[n] = acc[b];
+      std::snprintf(out[n].name, sizeof(out[n].name), "%s", kBucketName[b]);
+    }
+    ++n;
+  }
+  if (n_out) *n_out = n < max ? n : max;
+  return ok();
+}
+
+namespace {
+int elt_check(ming_ctx* c, const void* a, const void* b, int rows, int n) {
+  if (!c || !a || !b) return fail(MING_ERR_ARG, "null argument");
+  if (rows < 0 || n <= 0) return fail(MING_ERR_SHAPE, "bad rows / width");
+  return MING_OK;
+}
+}  // namespace
+
+int ming_swiglu(ming_ctx* c, const uint16_t* g, int64_t ldg, const uint16_t* u,
+                int64_t ldu, uint16_t* out, int64_t ldo, int rows, int n) {
+  int rc = elt_check(c, g, u, rows, n);
+  if (rc != MING_OK) return rc;
+  if (!out || n % 8 || ldg % 8 || ldu % 8 || ldo % 8 || !aligned(g, 16) ||
+      !aligned(u, 16) || !aligned(out, 16))
+    return fail(MING_ERR_SHAPE, "ming_swiglu: widths, strides and pointers must be 8-element aligned");
+  if (rows == 0) return ok();
+  DeviceGuard dg(c->device);
+  MING_HIP(profiled(c, kBSwiglu, 0.0, 6.0 * rows * n,
+                    [&] { return ming::launch_swiglu(g, ldg, u, ldu, out, ldo, rows, n,
+                                                     c->stream); }),
+           "swiglu launch");
+  c->eng.elementwise += 1;
+  return ok();
+}
+
+int ming_gated_residual(ming_ctx* c, uint16_t* h, int64_t ldh,
+                        const uint16_t* gate, const uint16_t* sub, int64_t lds,
+                        int rows, int n) {
+  int rc = elt_check(c, h, sub, rows, n);
+  if (rc != MING_OK) return rc;
+  if (!gate || n % 8 || ldh % 8 || lds % 8 || !aligned(h, 16) ||
+      !aligned(sub, 16) || !aligned(gate, 16))
+    return fail(MING_ERR_SHAPE, "ming_gated_residual: 8-element alignment required");
+  if (rows == 0) return ok();
+  DeviceGuard dg(c->device);
+  MING_HIP(profiled(c, kBResid, 0.0, 6.0 * rows * n,
+                    [&] { return ming::launch_residual(h, ldh, gate, sub, lds, rows, n,
+                                                       1, c->stream); }),
+           "gated_residual launch");
+  c->eng.elementwise += 1;
+  return ok();
+}
+
+int ming_residual_add(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
+                      int64_t lds, int rows, int n) {
+  int rc = elt_check(c, h, sub, rows, n);
+  if (rc != MING_OK) return rc;
+  if (n % 8 || ldh % 8 || lds % 8 || !aligned(h, 16) || !aligned(sub, 16))
+    return fail(MING_ERR_SHAPE, "ming_residual_add: 8-element alignment required");
+  if (rows == 0) return ok();
+  DeviceGuard dg(c->device);
+  MING_HIP(profiled(c, kBResid, 0.0, 6.0 * rows * n,
+                    [&] { return ming::launch_residual(h, ldh, nullptr, sub, lds, rows,
+                                                       n, 0, c->stream); }),
+           "residual_add launch");
+  c->eng.elementwise += 1;
+  return ok();
+}
+
+int ming_modulate(ming_ctx* c, const uint16_t* x, int64_t ldx,
+                  const uint16_t* scale, uint16_t* y, int64_t ldy, int rows,
+                  int n) {
+  int rc = elt_check(c, x, scale, rows, n);
+  if (rc != MING_OK) return rc;
+  if (!y) return fail(MING_ERR_ARG, "null argument");
+  if (rows == 0) return ok();
+  DeviceGuard dg(c->device);
+  MING_HIP(profiled(c, kBModulate, 0.0, 4.0 * rows * n + 2.0 * n,
+                    [&] { return ming::launch_modulate(x, ldx, scale, y, ldy, rows, n,
+                                                       c->stream); }),
+           "modulate launch");
+  c->eng.elementwise += 1;
+  return ok();
+}
+
+int ming_bias_act(ming_ctx* c, uint16_t* y, int64_t ldy, const uint16_t* bias,
+                  int rows, int n, int silu) {
+  int rc = elt_check(c, y, bias, rows, n);
+  if (rc != MING_OK) return rc;
+  if (rows == 0) return ok();
+  DeviceGuard dg(c->device);
+  MING_HIP(profiled(c, kBBias, 0.0, 4.0 * rows * n + 2.0 * n,
+                    [&] { return ming::launch_bias_act(y, ldy, bias, nullptr, rows, n,
+                                                       silu ? 1 : 0, c->stream); }),
+           "bias_act launch");
+  c->eng.elementwise += 1;
+  return ok();
+}
+
+int ming_silu(ming_ctx* c, const uint16_t* x, uint16_t* y, int n) {
+  int rc = elt_check(c, x, y, 1, n);
+  if (rc != MING_OK) return rc;
+  DeviceGuard dg(c->device);
+  MING_HIP(profiled(c, kBBias, 0.0, 4.0 * n,
+                    [&] { return ming::launch_bias_act(const_cast<uint16_t*>(x), n,
+                                                       nullptr, y, 1, n, 2, c->stream); }),
+           "silu launch");
+  c->eng.elementwise += 1;
+  return ok();
+}
+
+int ming_ln_modulate(ming_ctx* c, const uint16_t* x, int64_t ldx,
+                     const uint16_t* scale, uint16_t* y, int64_t ldy, int rows,
+                     int D, float eps) {
+  int rc = elt_check(c, x, scale, rows, D);
+  if (rc != MING_OK) return rc;
+  if (!y) return fail(MING_ERR_ARG, "null argument");
+  if (rows == 0) return ok();
+  DeviceGuard dg(c->device);
+  MING_HIP(profiled(c, kBLn, 0.0, 4.0 * rows * D,
+                    [&] { return ming::launch_ln_modulate(x, ldx, scale, y, ldy, rows, D,
+                                                          eps, c->stream); }),
+           "ln_modulate launch");
+  c->eng.elementwise += 1;
+  return ok();
+}
+
+int ming_quantize_pack(ming_ctx* c, const float* w, int N, int K, int bits,
+                       int group, uint32_t* codes, uint16_t* scales,
+                       uint16_t* biases) {
+  if (!c || !w || !codes || !scales || !biases)
+    return fail(MING_ERR_ARG, "ming_quantize_pack: null argument");
+  if ((bits != 4 && bits != 8) || group != 64 || N <= 0 || K <= 0 || K % 64)
+    return fail(MING_ERR_SHAPE, "ming_quantize_pack: bits 4/8, group 64, K % 64 == 0");
+  DeviceGuard dg(c->device);
+  MING_HIP(profiled(c, kBQuant, 0.0, 4.0 * N * K,
+                    [&] { return ming::launch_quantize(w, N, K, bits, codes, scales,
+                                                       biases, c->stream); }),
+           "quantize launch");
   return ok();
 }
 

@@ -38,6 +38,12 @@ class Engagement(C.Structure):
         return {k: getattr(self, k) for k, _ in self._fields_}
 
 
+class ProfileBucket(C.Structure):
+    _fields_ = [("name", C.c_char * 24), ("launches", C.c_int64),
+                ("ms", C.c_double), ("flops", C.c_double),
+                ("bytes", C.c_double)]
+
+
 def lib():
     """Load the built library (raises if it is not there)."""
     global _lib
@@ -76,6 +82,17 @@ def lib():
                              C.c_double, vp, vp], i32),
         "ming_qk_norm_rope": ([vp, vp, i64, i32, i32, i32, i32, i32, vp, vp,
                                vp, vp, f32], i32),
+        "ming_ctx_set_profiling": ([vp, i32], i32),
+        "ming_ctx_profile_collect": ([vp, C.POINTER(ProfileBucket), i32,
+                                      C.POINTER(i32)], i32),
+        "ming_swiglu": ([vp, vp, i64, vp, i64, vp, i64, i32, i32], i32),
+        "ming_gated_residual": ([vp, vp, i64, vp, vp, i64, i32, i32], i32),
+        "ming_residual_add": ([vp, vp, i64, vp, i64, i32, i32], i32),
+        "ming_modulate": ([vp, vp, i64, vp, vp, i64, i32, i32], i32),
+        "ming_bias_act": ([vp, vp, i64, vp, i32, i32, i32], i32),
+        "ming_silu": ([vp, vp, vp, i32], i32),
+        "ming_ln_modulate": ([vp, vp, i64, vp, vp, i64, i32, i32, f32], i32),
+        "ming_quantize_pack": ([vp, vp, i32, i32, i32, i32, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -148,6 +165,20 @@ class Ctx:
     def reset_engagement(self):
         _check(lib().ming_ctx_reset_engagement(self.h))
 
+    def set_profiling(self, on: bool = True):
+        _check(lib().ming_ctx_set_profiling(self.h, int(on)))
+
+    def profile_collect(self) -> dict:
+        """{bucket: {launches, ms, flops, bytes}} since the last collect."""
+        arr = (ProfileBucket * 32)()
+        n = C.c_int()
+        _check(lib().ming_ctx_profile_collect(self.h, arr, 32, C.byref(n)))
+        return {arr[i].name.decode(): {"launches": arr[i].launches,
+                                       "ms": arr[i].ms,
+                                       "flops": arr[i].flops,
+                                       "bytes": arr[i].bytes}
+                for i in range(n.value)}
+
     # ---- ops ----
     def lin(self, qw: "QWeight", x, y, M: int, scales=None, ldx=None,
             ldy=None):
@@ -176,6 +207,44 @@ class Ctx:
         _check(lib().ming_qk_norm_rope(self.h, _ptr(x), ld, q_col, k_col, rows,
                                        n_heads, head_dim, _ptr(wq), _ptr(wk),
                                        _ptr(cos_t), _ptr(sin_t), eps))
+
+
+    def swiglu(self, g, u, out, rows: int, n: int, ldg=None, ldu=None,
+               ldo=None):
+        _check(lib().ming_swiglu(self.h, _ptr(g), ldg or n, _ptr(u), ldu or n,
+                                 _ptr(out), ldo or n, rows, n))
+
+    def gated_residual(self, h, gate, sub, rows: int, n: int, ldh=None,
+                       lds=None):
+        _check(lib().ming_gated_residual(self.h, _ptr(h), ldh or n, _ptr(gate),
+                                         _ptr(sub), lds or n, rows, n))
+
+    def residual_add(self, h, sub, rows: int, n: int, ldh=None, lds=None):
+        _check(lib().ming_residual_add(self.h, _ptr(h), ldh or n, _ptr(sub),
+                                       lds or n, rows, n))
+
+    def modulate(self, x, scale, y, rows: int, n: int, ldx=None, ldy=None):
+        _check(lib().ming_modulate(self.h, _ptr(x), ldx or n, _ptr(scale),
+                                   _ptr(y), ldy or n, rows, n))
+
+    def bias_act(self, y, bias, rows: int, n: int, silu: bool = False,
+                 ldy=None):
+        _check(lib().ming_bias_act(self.h, _ptr(y), ldy or n, _ptr(bias), rows,
+                                   n, int(silu)))
+
+    def silu(self, x, y, n: int):
+        _check(lib().ming_silu(self.h, _ptr(x), _ptr(y), n))
+
+    def ln_modulate(self, x, scale, y, rows: int, D: int, eps: float = 1e-6,
+                    ldx=None, ldy=None):
+        _check(lib().ming_ln_modulate(self.h, _ptr(x), ldx or D, _ptr(scale),
+                                      _ptr(y), ldy or D, rows, D, eps))
+
+    def quantize_pack(self, w_f32, N: int, K: int, bits: int, codes, scales,
+                      biases, group: int = 64):
+        _check(lib().ming_quantize_pack(self.h, _ptr(w_f32), N, K, bits, group,
+                                        _ptr(codes), _ptr(scales),
+                                        _ptr(biases)))
 
 
 class QWeight:
