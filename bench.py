@@ -180,7 +180,9 @@ def main():
     assert eng["gemm_q4"] == 3 * args.steps and eng["lora_proj"] == 3 * args.steps, eng
     value = step_flops / (ms * 1e-3) / 1e12
 
-    q = prof["qproj.w4"]
+    qname = max((k for k in prof if k.startswith("qproj")),
+                key=lambda k: prof[k]["ms"])
+    q = prof[qname]
     achieved = q["flops"] / (q["ms"] * 1e-3) / 1e12
     kernels = {k: {"launches": v["launches"],
                    "avg_us": round(1e3 * v["ms"] / v["launches"], 2),
@@ -208,7 +210,7 @@ def main():
                    "parallelism": "1 GPU"},
         "mfma_util": round(value / PEAK_TFLOPS, 4),
         "forward_ms_1024": None,
-        "roofline": {"bound": "mfma", "kernel": "qproj.w4",
+        "roofline": {"bound": "mfma", "kernel": qname,
                      "achieved": round(achieved, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
                      "traffic": None,

@@ -62,7 +62,14 @@ typedef struct ming_engagement {
   int64_t attention;
   int64_t elementwise;
   uint64_t gemm_flops;  /* 2*M*N*K + sum_live 2*M*r*(K+N) per projection */
+  int64_t gemm_fast;    /* of the quantized projections, those on the fast route */
 } ming_engagement;
+
+/* Kernel routes for quantized projections. AUTO takes the fast route
+ * (fp16 activations, DMA-fed LDS ring, fragment dequant) whenever the
+ * weight's scales and biases are exact in fp16; GENERAL always takes the
+ * general kernel. Both compute the same function to the same bar. */
+enum { MING_ROUTE_AUTO = 0, MING_ROUTE_GENERAL = 1 };
 
 /* Per-launch kernel timing (HIP events around each launch, on the
  * context's stream), summed per kernel family -- the reference's profile
@@ -95,6 +102,7 @@ void* ming_ctx_stream(const ming_ctx* ctx);
 int ming_ctx_synchronize(ming_ctx* ctx);
 int ming_ctx_engagement(const ming_ctx* ctx, ming_engagement* out);
 int ming_ctx_reset_engagement(ming_ctx* ctx);
+int ming_ctx_set_route(ming_ctx* ctx, int route);
 /* Profiling on/off; collect waits for the stream, fills up to `max`
  * non-empty buckets and clears the records. */
 int ming_ctx_set_profiling(ming_ctx* ctx, int on);
@@ -127,6 +135,8 @@ int ming_qweight_concat(ming_ctx* ctx, int n_parts,
 int ming_qweight_destroy(ming_qweight* qw);
 /* 4, 8 or 16 (dense bf16); 0 on a null handle. */
 int ming_qweight_bits(const ming_qweight* qw);
+/* 1 when the weight can take the fast route (scales, biases fp16-exact). */
+int ming_qweight_fast(const ming_qweight* qw);
 int ming_qweight_shape(const ming_qweight* qw, int* N, int* K, int* n_segments);
 
 /* ---- runtime LoRA, bound at load (bind_loras_, ming-dit.cc:2918-3005) -------

@@ -15,6 +15,15 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
+@pytest.fixture(params=["auto", "general"], autouse=True)
+def route(request, ctx):
+    """Every projection test runs on both kernel routes."""
+    ctx.set_route(request.param)
+    ctx._route_param = request.param
+    yield request.param
+    ctx.set_route("auto")
+
+
 def _qw(ctx, pack, bits):
     if bits == 16:
         return m.QWeight.dense(ctx, pack["w"])
@@ -28,6 +37,10 @@ def _run(ctx, qw, x_dev, M, scales=None):
     ctx.lin(qw, x_dev, y, M, scales)
     sync()
     return from_dev(y)
+
+
+def route_is_auto(ctx):
+    return getattr(ctx, "_route_param", None) != "general"
 
 
 def _rel(orc, y_bf16, ref):
@@ -47,6 +60,9 @@ def test_base_projection_parity(ctx, orc, bits, M, N, K):
     eng = ctx.engagement()
     key = {4: "gemm_q4", 8: "gemm_q8", 16: "gemm_dense"}[bits]
     assert eng[key] == 1 and eng["lora_proj"] == 0 and eng["lora_xa"] == 0
+    want_fast = bits != 16 and route_is_auto(ctx)
+    assert qw.fast == (bits != 16)
+    assert eng["gemm_fast"] == (1 if want_fast else 0)
     ref = orc.proj(x, w)
     assert _rel(orc, y, ref) <= TOL
 
@@ -234,3 +250,25 @@ def test_config1_full_size(ctx, orc):
     assert _rel(orc, np.ascontiguousarray(y[rows]), ref) <= TOL
     y0 = _run(ctx, qw, xd, M, [0.0])
     assert np.array_equal(y0, _run(ctx, plain, xd, M))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_routes_agree(ctx, orc, bits, route):
+    """The fast and the general route compute the same function: both within
+    the bar, and within a fraction of it of each other."""
+    if route != "auto":
+        pytest.skip("compares the routes once")
+    M, N, K = 515, 768, 2048
+    x = to_dev(bf16(randn(101, (M, K))))
+    pack, w = make_weight(102, N, K, bits)
+    qw = _qw(ctx, pack, bits)
+    for s, r in enumerate((16, 64)):
+        A, B = make_lora(110 + 2 * s, N, K, r)
+        qw.bind_lora(s, A, B)
+    sc = [0.7, -0.4]
+    ctx.set_route("auto")
+    yf = _run(ctx, qw, x, M, sc)
+    ctx.set_route("general")
+    yg = _run(ctx, qw, x, M, sc)
+    ctx.set_route("auto")
+    assert orc.rel_l2(orc.bf16_to_f32(yf), orc.bf16_to_f32(yg)) < 5e-4

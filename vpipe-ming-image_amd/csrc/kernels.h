@@ -111,7 +111,18 @@ hipError_t launch_quantize(const float* w, int N, int K, int bits,
                            uint32_t* codes, uint16_t* scales, uint16_t* biases,
                            hipStream_t s);
 
+// ---- the fast quantized route (qproj_fast.hip) --------------------------------
+// x is fp16 (carrying bf16 values), a.codes / a.sb the fast resident layout.
+hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s);
+hipError_t launch_repack_fast(int bits, const uint32_t* codes,
+                              const uint16_t* scales, const uint16_t* biases,
+                              int N, int K, uint32_t* codes_f, uint32_t* sbf,
+                              int* inexact, hipStream_t s);
+hipError_t launch_bf16_to_f16(const uint16_t* x, long long ldx, uint16_t* y,
+                              long long ldy, int rows, int K, hipStream_t s);
+
 hipError_t validate_qproj_kernels();
+hipError_t validate_qproj_fast_kernels();
 hipError_t validate_norm_kernels();
 hipError_t validate_elementwise_kernels();
 

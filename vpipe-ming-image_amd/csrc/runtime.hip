@@ -61,6 +61,9 @@ struct ming_ctx {
   ming_engagement eng{};
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  void* xh = nullptr;          // fp16 copy of the projection input
+  size_t xh_bytes = 0;
+  int route = MING_ROUTE_AUTO;
   int live_weights = 0;   // a context outlives every weight made on it
   // Per-launch HIP-event timing (ming_ctx_set_profiling), by bucket.
   bool profiling = false;
@@ -74,11 +77,12 @@ namespace {
 // Profile buckets: one per kernel family (the reference's per-category
 // marks, ming-dit.cc:1689-1717, as HIP events around each launch).
 enum Bucket {
-  kBQ4, kBQ8, kBDense, kBXa, kBRms, kBQkRope, kBRopeTab, kBSwiglu, kBResid,
+  kBQ4, kBQ8, kBDense, kBF4, kBF8, kBCvt, kBXa, kBRms, kBQkRope, kBRopeTab, kBSwiglu, kBResid,
   kBModulate, kBBias, kBLn, kBQuant, kBAttn, kBCount
 };
 const char* const kBucketName[kBCount] = {
-    "qproj.w4", "qproj.w8", "qproj.dense", "lora_xa", "rmsnorm",
+    "qproj.w4", "qproj.w8", "qproj.dense", "qproj_fast.w4", "qproj_fast.w8",
+    "cvt_f16", "lora_xa", "rmsnorm",
     "qk_norm_rope", "rope_table", "swiglu", "residual", "modulate",
     "bias_act", "ln_modulate", "quantize", "attention"};
 
@@ -133,8 +137,11 @@ int round_up(int v, int m) { return (v + m - 1) / m * m; }
 struct ming_qweight {
   ming_ctx* ctx = nullptr;
   int N = 0, K = 0, bits = 0, group = 64;
-  uint32_t* codes_t = nullptr;
+  uint32_t* codes_t = nullptr;   // general route: [kt][n][w] + bf16 (s, b)
   uint32_t* sb = nullptr;
+  uint32_t* codes_f = nullptr;   // fast route: fragment-ordered codes
+  uint32_t* sbf = nullptr;       //   + fp16 (s, b)
+  bool fast = false;             // every scale and bias exact in fp16
   uint16_t* w16 = nullptr;
   std::vector<Segment> segs;
   // Stacked adapter factors, rebuilt when a binding changes:
@@ -227,6 +234,19 @@ int ensure_scratch(ming_ctx* c, size_t bytes) {
   return MING_OK;
 }
 
+int ensure_xh(ming_ctx* c, size_t bytes) {
+  if (bytes <= c->xh_bytes) return MING_OK;
+  MING_HIP(hipStreamSynchronize(c->stream), "scratch grow sync");
+  if (c->xh) (void)hipFree(c->xh);
+  c->xh = nullptr;
+  c->xh_bytes = 0;
+  size_t want = std::max(bytes, (size_t)1 << 20);
+  if (hipMalloc(&c->xh, want) != hipSuccess)
+    return fail(MING_ERR_ALLOC, "fp16 activation scratch allocation failed");
+  c->xh_bytes = want;
+  return MING_OK;
+}
+
 // Copy `bytes` from host or device into a fresh device buffer.
 int upload(ming_ctx* c, void** dst, const void* src, size_t bytes,
            int src_on_device) {
@@ -251,6 +271,8 @@ void destroy_qweight(ming_qweight* q) {
   (void)hipStreamSynchronize(q->ctx->stream);
   if (q->codes_t) (void)hipFree(q->codes_t);
   if (q->sb) (void)hipFree(q->sb);
+  if (q->codes_f) (void)hipFree(q->codes_f);
+  if (q->sbf) (void)hipFree(q->sbf);
   if (q->w16) (void)hipFree(q->w16);
   for (auto& sg : q->segs)
     for (auto& b : sg.slot) {
@@ -283,6 +305,7 @@ int ming_ctx_create(int device, void* hip_stream, ming_ctx** out) {
   hipError_t e = ming::validate_qproj_kernels();
   if (e == hipSuccess) e = ming::validate_norm_kernels();
   if (e == hipSuccess) e = ming::validate_elementwise_kernels();
+  if (e == hipSuccess) e = ming::validate_qproj_fast_kernels();
   if (e != hipSuccess)
     return fail(MING_ERR_KERNEL,
                 std::string("kernel validation failed on this device (the "
@@ -312,6 +335,7 @@ int ming_ctx_destroy(ming_ctx* c) {
   DeviceGuard g(c->device);
   (void)hipStreamSynchronize(c->stream);
   if (c->scratch) (void)hipFree(c->scratch);
+  if (c->xh) (void)hipFree(c->xh);
   for (auto& rec : c->recs) {
     (void)hipEventDestroy(rec.a);
     (void)hipEventDestroy(rec.b);
@@ -382,13 +406,27 @@ int ming_qweight_create(ming_ctx* c, int N, int K, int bits, int group,
   if (rc == MING_OK) rc = upload(c, &db, biases, (size_t)N * G * 2, src_on_device);
   hipError_t e = hipSuccess;
   if (rc == MING_OK) {
+    int* flag = nullptr;
     e = hipMalloc(&q->codes_t, words * 4);
     if (e == hipSuccess) e = hipMalloc(&q->sb, (size_t)N * G * 4);
+    if (e == hipSuccess) e = hipMalloc(&q->codes_f, words * 4);
+    if (e == hipSuccess) e = hipMalloc(&q->sbf, (size_t)N * G * 4);
+    if (e == hipSuccess) e = hipMalloc(&flag, sizeof(int));
+    if (e == hipSuccess) e = hipMemsetAsync(flag, 0, sizeof(int), c->stream);
     if (e == hipSuccess)
       e = ming::launch_repack(bits, (const uint32_t*)dc, (const uint16_t*)ds,
                               (const uint16_t*)db, N, K, q->codes_t, q->sb,
                               c->stream);
+    if (e == hipSuccess)
+      e = ming::launch_repack_fast(bits, (const uint32_t*)dc, (const uint16_t*)ds,
+                                   (const uint16_t*)db, N, K, q->codes_f, q->sbf,
+                                   flag, c->stream);
+    int inexact = 1;
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(&inexact, flag, sizeof(int), hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (flag) (void)hipFree(flag);
+    q->fast = (e == hipSuccess && inexact == 0);
     if (e != hipSuccess) rc = hip_fail(e, "ming_qweight_create: repack");
   }
   if (dc) (void)hipFree(dc);
@@ -468,6 +506,10 @@ int ming_qweight_concat(ming_ctx* c, int n_parts, ming_qweight* const* parts,
   } else {
     chk(hipMalloc(&q->codes_t, (size_t)N * K * bits / 8), "concat alloc");
     chk(hipMalloc(&q->sb, (size_t)N * (K / 64) * 4), "concat alloc");
+    chk(hipMalloc(&q->codes_f, (size_t)N * K * bits / 8), "concat alloc");
+    chk(hipMalloc(&q->sbf, (size_t)N * (K / 64) * 4), "concat alloc");
+    q->fast = true;
+    for (int i = 0; i < n_parts; ++i) q->fast = q->fast && parts[i]->fast;
   }
   q->segs.resize(n_parts);
   int nb = 0;
@@ -486,6 +528,13 @@ int ming_qweight_concat(ming_ctx* c, int n_parts, ming_qweight* const* parts,
                            (size_t)p->N * wpr * 4, (size_t)KT,
                            hipMemcpyDeviceToDevice, s), "concat copy");
       chk(hipMemcpy2DAsync(q->sb + nb, (size_t)N * 4, p->sb, (size_t)p->N * 4,
+                           (size_t)p->N * 4, (size_t)KT,
+                           hipMemcpyDeviceToDevice, s), "concat copy");
+      chk(hipMemcpy2DAsync(q->codes_f + (size_t)nb * wpr, (size_t)N * wpr * 4,
+                           p->codes_f, (size_t)p->N * wpr * 4,
+                           (size_t)p->N * wpr * 4, (size_t)KT,
+                           hipMemcpyDeviceToDevice, s), "concat copy");
+      chk(hipMemcpy2DAsync(q->sbf + nb, (size_t)N * 4, p->sbf, (size_t)p->N * 4,
                            (size_t)p->N * 4, (size_t)KT,
                            hipMemcpyDeviceToDevice, s), "concat copy");
     }
@@ -691,9 +740,21 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
              "lora_xa launch");
     c->eng.lora_xa += 1;
   }
+  const bool fast = q->bits != 16 && q->fast && c->route != MING_ROUTE_GENERAL;
   qa.x = x; qa.ldx = ldx; qa.codes = q->codes_t; qa.sb = q->sb; qa.w16 = q->w16;
   qa.y = y; qa.ldy = ldy; qa.M = M; qa.N = q->N; qa.K = q->K;
   qa.t = T; qa.ldt = t_cols > 0 ? t_cols : 0; qa.nseg = nseg;
+  if (fast) {
+    // The fast route reads x as fp16 carrying the same (bf16) values.
+    int rc = ensure_xh(c, (size_t)M * q->K * 2);
+    if (rc != MING_OK) return rc;
+    uint16_t* xh = (uint16_t*)c->xh;
+    MING_HIP(profiled(c, kBCvt, 0.0, 4.0 * M * q->K,
+                      [&] { return ming::launch_bf16_to_f16(x, ldx, xh, q->K, M,
+                                                            q->K, c->stream); }),
+             "bf16->fp16 launch");
+    qa.x = xh; qa.ldx = q->K; qa.codes = q->codes_f; qa.sb = q->sbf;
+  }
   const double base_flops = 2.0 * M * (double)q->N * q->K;
   double tail_flops = 0.0;
   for (int si = 0; si < nseg; ++si)
@@ -705,11 +766,16 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
   const double wbytes = q->bits == 16
                             ? 2.0 * q->N * q->K
                             : (double)q->N * q->K * q->bits / 8 + 4.0 * q->N * (q->K / 64);
-  const int bk = q->bits == 4 ? kBQ4 : (q->bits == 8 ? kBQ8 : kBDense);
+  const int bk = fast ? (q->bits == 4 ? kBF4 : kBF8)
+                      : (q->bits == 4 ? kBQ4 : (q->bits == 8 ? kBQ8 : kBDense));
   MING_HIP(profiled(c, bk, base_flops + tail_flops,
                     2.0 * M * q->K + wbytes + 2.0 * M * q->N,
-                    [&] { return ming::launch_qproj(q->bits, qa, c->stream); }),
+                    [&] {
+                      return fast ? ming::launch_qproj_fast(q->bits, qa, c->stream)
+                                  : ming::launch_qproj(q->bits, qa, c->stream);
+                    }),
            "qproj launch");
+  if (fast) c->eng.gemm_fast += 1;
   if (q->bits == 4) c->eng.gemm_q4 += 1;
   else if (q->bits == 8) c->eng.gemm_q8 += 1;
   else c->eng.gemm_dense += 1;
@@ -784,6 +850,16 @@ int ming_qk_norm_rope(ming_ctx* c, uint16_t* x, int64_t ld, int q_col, int k_col
   return ok();
 }
 
+
+int ming_ctx_set_route(ming_ctx* c, int route) {
+  if (!c) return fail(MING_ERR_ARG, "null context");
+  if (route != MING_ROUTE_AUTO && route != MING_ROUTE_GENERAL)
+    return fail(MING_ERR_ARG, "ming_ctx_set_route: unknown route");
+  c->route = route;
+  return ok();
+}
+
+int ming_qweight_fast(const ming_qweight* q) { return q && q->fast ? 1 : 0; }
 
 int ming_ctx_set_profiling(ming_ctx* c, int on) {
   if (!c) return fail(MING_ERR_ARG, "null context");

@@ -32,7 +32,7 @@ class Engagement(C.Structure):
                 ("lora_xa", C.c_int64), ("rmsnorm", C.c_int64),
                 ("qk_norm_rope", C.c_int64), ("rope_table", C.c_int64),
                 ("attention", C.c_int64), ("elementwise", C.c_int64),
-                ("gemm_flops", C.c_uint64)]
+                ("gemm_flops", C.c_uint64), ("gemm_fast", C.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -83,6 +83,8 @@ def lib():
         "ming_qk_norm_rope": ([vp, vp, i64, i32, i32, i32, i32, i32, vp, vp,
                                vp, vp, f32], i32),
         "ming_ctx_set_profiling": ([vp, i32], i32),
+        "ming_ctx_set_route": ([vp, i32], i32),
+        "ming_qweight_fast": ([vp], i32),
         "ming_ctx_profile_collect": ([vp, C.POINTER(ProfileBucket), i32,
                                       C.POINTER(i32)], i32),
         "ming_swiglu": ([vp, vp, i64, vp, i64, vp, i64, i32, i32], i32),
@@ -164,6 +166,10 @@ class Ctx:
 
     def reset_engagement(self):
         _check(lib().ming_ctx_reset_engagement(self.h))
+
+    def set_route(self, route: str = "auto"):
+        """'auto' (fast route when the weight allows it) or 'general'."""
+        _check(lib().ming_ctx_set_route(self.h, {"auto": 0, "general": 1}[route]))
 
     def set_profiling(self, on: bool = True):
         _check(lib().ming_ctx_set_profiling(self.h, int(on)))
@@ -259,6 +265,7 @@ class QWeight:
                                         C.byref(S)))
         self.N, self.K, self.n_segments = N.value, K.value, S.value
         self.bits = lib().ming_qweight_bits(h)
+        self.fast = bool(lib().ming_qweight_fast(h))
 
     @classmethod
     def quantized(cls, ctx: Ctx, codes, scales, biases, bits: int,
