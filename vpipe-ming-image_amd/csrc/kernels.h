@@ -118,6 +118,11 @@ hipError_t launch_repack_fast(int bits, const uint32_t* codes,
                               const uint16_t* scales, const uint16_t* biases,
                               int N, int K, uint32_t* codes_f, uint32_t* sbf,
                               int* inexact, hipStream_t s);
+// x.A_live^T with split-K: `part` holds kslices * M * n_cols f32 (unused
+// when kslices == 1).
+int lora_xa_fast_slices(int M, int n_cols, int K);
+hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
+                               hipStream_t s);
 hipError_t launch_bf16_to_f16(const uint16_t* x, long long ldx, uint16_t* y,
                               long long ldy, int rows, int K, hipStream_t s);
 

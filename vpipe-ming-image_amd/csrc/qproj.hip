@@ -33,8 +33,10 @@ namespace {
 constexpr int BM = kQpBM, BN = kQpBN, BK = kQpBK, NT = kQpThreads;
 constexpr int CH = BK / 8;  // 16-byte chunks per tile row
 
+// 16-byte chunks XOR-swizzled by (row >> 1) & 7: a ds_read_b128 serves 16
+// lanes per cycle on gfx950's 64 banks, and 128-B rows pair up per bank line.
 __device__ __forceinline__ int swz(int row, int c) {
-  return row * CH + (c ^ (row & 7));
+  return row * CH + (c ^ ((row >> 1) & 7));
 }
 
 // Logical tile for this block: XCD-contiguous ranges, then grouped raster

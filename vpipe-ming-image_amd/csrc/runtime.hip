@@ -63,6 +63,8 @@ struct ming_ctx {
   size_t scratch_bytes = 0;
   void* xh = nullptr;          // fp16 copy of the projection input
   size_t xh_bytes = 0;
+  void* part = nullptr;        // split-K partials of the stacked x.A GEMM
+  size_t part_bytes = 0;
   int route = MING_ROUTE_AUTO;
   int live_weights = 0;   // a context outlives every weight made on it
   // Per-launch HIP-event timing (ming_ctx_set_profiling), by bucket.
@@ -234,6 +236,19 @@ int ensure_scratch(ming_ctx* c, size_t bytes) {
   return MING_OK;
 }
 
+int ensure_part(ming_ctx* c, size_t bytes) {
+  if (bytes <= c->part_bytes) return MING_OK;
+  MING_HIP(hipStreamSynchronize(c->stream), "scratch grow sync");
+  if (c->part) (void)hipFree(c->part);
+  c->part = nullptr;
+  c->part_bytes = 0;
+  size_t want = std::max(bytes, (size_t)1 << 20);
+  if (hipMalloc(&c->part, want) != hipSuccess)
+    return fail(MING_ERR_ALLOC, "split-K partial scratch allocation failed");
+  c->part_bytes = want;
+  return MING_OK;
+}
+
 int ensure_xh(ming_ctx* c, size_t bytes) {
   if (bytes <= c->xh_bytes) return MING_OK;
   MING_HIP(hipStreamSynchronize(c->stream), "scratch grow sync");
@@ -336,6 +351,7 @@ int ming_ctx_destroy(ming_ctx* c) {
   (void)hipStreamSynchronize(c->stream);
   if (c->scratch) (void)hipFree(c->scratch);
   if (c->xh) (void)hipFree(c->xh);
+  if (c->part) (void)hipFree(c->part);
   for (auto& rec : c->recs) {
     (void)hipEventDestroy(rec.a);
     (void)hipEventDestroy(rec.b);
@@ -734,9 +750,22 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
         if (b.rank > 0 && scales && scales[sl] != 0.0f)
           xa_flops += 2.0 * M * b.rank * (double)q->K;
       }
+    const bool xa_fast = c->route != MING_ROUTE_GENERAL && ldx % 8 == 0;
+    int ks = 1;
+    if (xa_fast) {
+      ks = ming::lora_xa_fast_slices(M, t_cols, q->K);
+      if (ks > 1) {
+        int rc = ensure_part(c, (size_t)ks * M * t_cols * 4);
+        if (rc != MING_OK) return rc;
+      }
+    }
     MING_HIP(profiled(c, kBXa, xa_flops,
                       2.0 * M * q->K + 2.0 * t_cols * (double)q->K + 2.0 * M * t_cols,
-                      [&] { return ming::launch_lora_xa(xa, c->stream); }),
+                      [&] {
+                        return xa_fast ? ming::launch_lora_xa_fast(xa, (float*)c->part,
+                                                                   ks, c->stream)
+                                       : ming::launch_lora_xa(xa, c->stream);
+                      }),
              "lora_xa launch");
     c->eng.lora_xa += 1;
   }

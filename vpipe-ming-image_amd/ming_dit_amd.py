@@ -13,7 +13,9 @@ import os
 import weakref
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libming_dit_amd.so")
+# MING_DIT_AMD_LIB points at another build of the same library (A/B runs).
+LIB_PATH = os.environ.get("MING_DIT_AMD_LIB",
+                          os.path.join(_HERE, "libming_dit_amd.so"))
 HEADER = os.path.join(os.path.dirname(_HERE), "include", "ming_dit_amd.h")
 MAX_SLOTS = 8
 
