@@ -35,6 +35,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
+// The same round-to-nearest-even pair conversion by gfx950's
+// v_cvt_pk_bf16_f32 (one instruction for two values). Identical to
+// pack_bf16x2 for every non-NaN input; a NaN stays a quiet NaN.
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  const bf16x2v v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // Two bf16 (one u32) -> two fp16 (one u32). Exact for every value inside
 // fp16's range, so the rounding mode of the packed conversion is moot.
 __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u) {

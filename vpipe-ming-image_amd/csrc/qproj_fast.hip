@@ -65,6 +65,40 @@ __device__ __forceinline__ void dma4(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, lds_wave_base, 4, 0, 0);
 }
 
+// The same DMA written as inline asm, for rings whose waits are all
+// explicit: the compiler then sees no LDS store it must order reads
+// against, so it cannot add a drain of its own (its alias tracking of LDS
+// DMA gives up at loop joins and would wait for vmcnt(0)). M0 carries the
+// wave's LDS byte address; the s_nop covers the M0 -> LDS-DMA hazard.
+// Correctness rests on the ring's own waits: ring_wait<N>() below, which
+// also orders every LDS access against the DMAs through its memory clobber.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_asm(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma4_asm(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(src), "s"(lds) : "m0");
+}
+#pragma clang diagnostic pop
+
+// LDS byte address of a __shared__ object: the low half of its generic
+// address is the offset inside the workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// Ring barrier with its vmcnt: this wave's DMAs except the newest N have
+// landed, its LDS reads are complete, then the workgroup barrier. After it
+// every wave's older DMAs are visible and every wave is done reading.
+template <int N>
+__device__ __forceinline__ void ring_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(N) : "memory");
+}
+
 // 8 codes (one w4 word) -> 8 fp16 dequantized values. The word's nibbles
 // are ordered {k0,k4,k1,k5,k2,k6,k3,k7}, so lo = w & 0x0F0F0F0F holds
 // k0..k3 one per byte and hi = (w >> 4) & 0x0F0F0F0F holds k4..k7; one
@@ -141,20 +175,9 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
   constexpr int CPR = BITS == 4 ? 2 : 4;         // code chunks per row
   constexpr int WDMA = WCH / 256;                // code DMAs per wave per stage
   constexpr int PER = 8 + WDMA + 1;              // DMAs per wave per base stage
-  // One __shared__ object per stage ([x 32 KB | codes | (s, b)]): the
-  // compiler tracks LDS DMA per object, and three objects stay within
-  // what it tracks, so a read of one stage never waits on another's DMA.
+  // One __shared__ object per stage: [x 32 KB | codes | (s, b)].
   constexpr int STG = BM * 8 + WCH + BN / 4;
   __shared__ uint4 st0[STG], st1[STG], st2[STG];
-  uint4* const sX0 = st0;
-  uint4* const sX1 = st1;
-  uint4* const sX2 = st2;
-  uint4* const sW0 = st0 + BM * 8;
-  uint4* const sW1 = st1 + BM * 8;
-  uint4* const sW2 = st2 + BM * 8;
-  uint32_t* const sS0 = reinterpret_cast<uint32_t*>(st0 + BM * 8 + WCH);
-  uint32_t* const sS1 = reinterpret_cast<uint32_t*>(st1 + BM * 8 + WCH);
-  uint32_t* const sS2 = reinterpret_cast<uint32_t*>(st2 + BM * 8 + WCH);
 
   // Waves split N only: wave w owns output columns [64w, 64w+64) for all
   // 256 rows (2 x 8 tiles of 32x32), so every weight fragment is
@@ -201,14 +224,21 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
   int sn = n0 + 64 * wave + lane;
   sn = sn < nlast ? sn : nlast;
 
-  auto issue = [&](int kt, uint4* X, uint4* W, uint32_t* S) {
+  // The stage's DMAs in three groups (x rows 0-127, x rows 128-255, codes +
+  // (s, b)), issued one group per k16 step of the stage before.
+  auto issue_grp = [&](int g, int kt, const uint4* B) {
+    if (g < 2) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      dma16(x16 + xoff[i] + kt * BK, X + 64 * (8 * wave + i));
+      for (int i = 4 * g; i < 4 * g + 4; ++i)
+        dma16_asm(x16 + xoff[i] + kt * BK, lds_addr(B + 64 * (8 * wave + i)));
+    } else {
 #pragma unroll
-    for (int i = 0; i < WDMA; ++i)
-      dma16(codes + (long long)kt * a.N * CPR + woff[i], W + 64 * (WDMA * wave + i));
-    dma4(a.sb + (long long)kt * a.N + sn, S + 64 * wave);
+      for (int i = 0; i < WDMA; ++i)
+        dma16_asm(codes + (long long)kt * a.N * CPR + woff[i],
+                  lds_addr(B + BM * 8 + 64 * (WDMA * wave + i)));
+      dma4_asm(a.sb + (long long)kt * a.N + sn,
+               lds_addr(reinterpret_cast<const uint32_t*>(B + BM * 8 + WCH) + 64 * wave));
+    }
   };
 
   floatx16_t acc[2][8];
@@ -219,49 +249,67 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
 
-  // One stage of MFMA work: code words + (s, b) for the wave's 2 n-tiles,
-  // then 4 k16 steps, each reading and dequantizing the next step's
-  // fragments beside this step's 16 MFMAs. The interleave is pinned with
-  // scheduling-group barriers: left alone, the scheduler (at the VGPR
-  // limit) sinks each fragment read next to its MFMA and exposes the LDS
-  // latency every few MFMAs. `pre` runs inside step 0 (the ring's DMA
-  // issue), interleaved with its MFMAs.
-  auto compute = [&](const uint4* X, const uint4* W, const uint32_t* S, auto&& pre) {
-    uint4 wc[2][CPR / 2];
-    half2v s2[2], b2[2];
+  // Stage state in registers: the code words and (s, b) of the wave's two
+  // n-tiles, and the current k16 step's operands.
+  uint4 wc[2][CPR / 2];
+  half2v s2[2], b2[2];
+  uint4 wa[2], xb[8];
+
+  auto load_ws = [&](const uint4* B, uint4 (&wcv)[2][CPR / 2], half2v (&s2v)[2],
+                     half2v (&b2v)[2]) {
+    const uint4* W = B + BM * 8;
+    const uint32_t* S = reinterpret_cast<const uint32_t*>(B + BM * 8 + WCH);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int n = 64 * wave + 32 * j + fr;
 #pragma unroll
       for (int h = 0; h < CPR / 2; ++h)
-        wc[j][h] = W[wchunk<CPR>(n, fk * (CPR / 2) + h)];
+        wcv[j][h] = W[wchunk<CPR>(n, fk * (CPR / 2) + h)];
       const uint32_t sb = S[n];
-      s2[j] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(sb, sb, 0x01000100u));
-      b2[j] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(sb, sb, 0x03020302u));
+      s2v[j] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(sb, sb, 0x01000100u));
+      b2v[j] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(sb, sb, 0x03020302u));
     }
-    auto deq = [&](int j, int kk) -> uint4 {
-      if constexpr (BITS == 4) {
-        return deq_w4((&wc[j][0].x)[kk], s2[j], b2[j]);
-      } else {
-        const uint32_t* w = &wc[j][kk >> 1].x;
-        return deq_w8(w[(kk & 1) * 2], w[(kk & 1) * 2 + 1], s2[j], b2[j]);
-      }
-    };
-    uint4 wa[2], xb[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xb[i] = X[swz8(32 * i + fr, fk)];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) wa[j] = deq(j, 0);
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto deq = [&](const uint4 (&wcv)[2][CPR / 2], const half2v (&s2v)[2],
+                 const half2v (&b2v)[2], int j, int kk) -> uint4 {
+    if constexpr (BITS == 4) {
+      return deq_w4((&wcv[j][0].x)[kk], s2v[j], b2v[j]);
+    } else {
+      const uint32_t* w = &wcv[j][kk >> 1].x;
+      return deq_w8(w[(kk & 1) * 2], w[(kk & 1) * 2 + 1], s2v[j], b2v[j]);
+    }
+  };
+
+  // One stage, software-pipelined across the stage boundary. Steps 0-2
+  // read and dequantize the next step's fragments beside the current
+  // step's 16 MFMAs and issue one DMA group of stage kt+2 into Pv (the
+  // buffer stage kt-1 left). Between steps 2 and 3 the wave waits for its
+  // stage kt+1 DMAs and the workgroup meets at the barrier: stage kt+1 is
+  // in LDS and nobody reads stage kt's buffer again. Step 3's MFMAs then
+  // carry the next stage's code / (s, b) reads, its first x fragments and
+  // their dequantization, so no stage starts with an LDS round trip.
+  // Interleave pinned with scheduling-group barriers (0x008 MFMA, 0x100 DS
+  // read, 0x002 VALU). Past the last stage the DMA re-reads stage KT-1 into
+  // a buffer nothing reads, so every stage issues and waits alike.
+  auto body = [&](int kt, const uint4* C, const uint4* Nx, const uint4* Pv) {
+    const int nk = kt + 2 < KT ? kt + 2 : KT - 1;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       uint4 wn_[2], xn_[8];
-      if (kk == 0) pre();
+      uint4 wcn[2][CPR / 2];
+      half2v s2n[2], b2n[2];
       if (kk < 3) {
+        issue_grp(kk, nk, Pv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xn_[i] = X[swz8(32 * i + fr, 2 * (kk + 1) + fk)];
+        for (int i = 0; i < 8; ++i) xn_[i] = C[swz8(32 * i + fr, 2 * (kk + 1) + fk)];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) wn_[j] = deq(j, kk + 1);
+        for (int j = 0; j < 2; ++j) wn_[j] = deq(wc, s2, b2, j, kk + 1);
+      } else {
+        load_ws(Nx, wcn, s2n, b2n);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xn_[i] = Nx[swz8(32 * i + fr, fk)];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) wn_[j] = deq(wcn, s2n, b2n, j, 0);
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -270,14 +318,6 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
           acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
               __builtin_bit_cast(half8_t, wa[j]), __builtin_bit_cast(half8_t, xb[i]),
               acc[j][i], 0, 0, 0);
-      if (kk == 0) {
-        // the ring's DMAs (with their address and M0 setup), one per MFMA
-#pragma unroll
-        for (int g = 0; g < PER; ++g) {
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-        }
-      }
       if (kk < 3) {
 #pragma unroll
         for (int g = 0; g < 8; ++g) {
@@ -289,48 +329,69 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
           __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // 4 VALU
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
         }
+      } else {
+        constexpr int NDS = 8 + 2 * (CPR / 2) + 2;
+        static_assert(NDS >= 10 && NDS <= 20, "step-3 DS reads per MFMA pin");
+#pragma unroll
+        for (int g = 0; g < NDS - 10; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+#pragma unroll
+        for (int g = NDS - 10; g < 10; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < 6; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (kk < 3) {
+      if (kk == 2) {
+        ring_wait<PER>();                      // stage kt+1 landed, kt done
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) wa[j] = wn_[j];
+      for (int j = 0; j < 2; ++j) wa[j] = wn_[j];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xb[i] = xn_[i];
+      for (int i = 0; i < 8; ++i) xb[i] = xn_[i];
+      if (kk == 3) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int h = 0; h < CPR / 2; ++h) wc[j][h] = wcn[j][h];
+          s2[j] = s2n[j];
+          b2[j] = b2n[j];
+        }
       }
     }
   };
 
-  // ---- base ring: stage kt lives in buffer kt % 3 ----
-  // Iteration kt: wait for stage kt (this wave's DMAs; stage kt+1 stays in
-  // flight), barrier (every wave's stage kt landed AND every wave is done
-  // reading buffer (kt+2)%3 from iteration kt-1), issue stage kt+2 beside
-  // stage kt's first MFMAs, compute stage kt. Every iteration issues and
-  // waits the same way -- past the end the "next" stage re-reads stage
-  // KT-1 into a buffer nothing reads -- so the waits are one static vmcnt
-  // and the compiler adds no drain of its own.
-  auto step = [&](int kt, uint4* Xc, uint4* Wc, uint32_t* Sc, uint4* Xn,
-                  uint4* Wn, uint32_t* Sn) {
-    __builtin_amdgcn_s_waitcnt(vm_wait(PER));   // stage kt done
-    ring_barrier();
-    const int nk = kt + 2 < KT ? kt + 2 : KT - 1;
-    if (kt < KT) {
-      compute(Xc, Wc, Sc, [&] { issue(nk, Xn, Wn, Sn); });
-    } else {
-      issue(nk, Xn, Wn, Sn);
-    }
-  };
+  // Prologue: stages 0 and 1 in flight, wait for stage 0, load its state.
+#pragma unroll
+  for (int g = 0; g < 3; ++g) issue_grp(g, 0, st0);
+#pragma unroll
+  for (int g = 0; g < 3; ++g) issue_grp(g, KT > 1 ? 1 : 0, st1);
+  ring_wait<PER>();
+  load_ws(st0, wc, s2, b2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xb[i] = st0[swz8(32 * i + fr, fk)];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) wa[j] = deq(wc, s2, b2, j, 0);
 
-  issue(0, sX0, sW0, sS0);
-  issue(KT > 1 ? 1 : 0, sX1, sW1, sS1);
-  // Three steps per trip, all issuing and waiting (a step past KT only
-  // skips its MFMA work), so no path through the loop leaves a different
-  // set of DMAs in flight.
-  for (int kt = 0; kt < KT; kt += 3) {
-    step(kt, sX0, sW0, sS0, sX2, sW2, sS2);
-    step(kt + 1, sX1, sW1, sS1, sX0, sW0, sS0);
-    step(kt + 2, sX2, sW2, sS2, sX1, sW1, sS1);
+  // Stage kt lives in buffer kt % 3; three stages per trip, the remainder
+  // (KT % 3) after the loop, so the loop body has no branch.
+  int kt = 0;
+  for (; kt + 3 <= KT; kt += 3) {
+    body(kt, st0, st1, st2);
+    body(kt + 1, st1, st2, st0);
+    body(kt + 2, st2, st0, st1);
   }
-  __builtin_amdgcn_s_waitcnt(vm_wait(0));       // drain the ring
+  if (KT - kt >= 1) body(kt, st0, st1, st2);
+  if (KT - kt == 2) body(kt + 1, st1, st2, st0);
+  ring_wait<0>();                               // drained; LDS free
 
   // ---- LoRA tail: T and gathered B chunks of 32 ranks, same ring ----
   int sg = 0;
@@ -345,7 +406,8 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     const uint16_t* __restrict__ Bp = a.seg[sg].B;
     // the first live group of the segment: a finite source for padding
     // groups (their T columns are exactly 0)
-    const int g_safe = a.grp[grp0];
+    const int g_safe =
+        (int16_t)(reinterpret_cast<const uint32_t*>(a.grp)[grp0 >> 1] & 0xffffu);
     long long toff[4];
     long long boff[4];
     int bc[4];
@@ -362,68 +424,128 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
       boff[i] = (long long)(n - seg_nb) * ldb;
       bc[i] = c;
     }
-    // T region = first 16 KB of the stage's x slot, B region = second.
-    auto issue_t = [&](int ch, uint4* X) {
+    // T region = first 16 KB of the stage buffer, B region = second. The
+    // two 16-rank groups of a chunk are wave-uniform (scalar loads).
+    auto issue_t = [&](int ch, const uint4* X) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        dma16(a.t + toff[i] + 32 * ch, X + 64 * (4 * wave + i));
+        dma16_asm(a.t + toff[i] + 32 * ch, lds_addr(X + 64 * (4 * wave + i)));
+      // The chunk's two groups are one aligned dword of the table (a
+      // segment's groups start at a multiple of 4): a wave-uniform scalar
+      // load (lgkmcnt), never a VMEM load the compiler would wait for with
+      // vmcnt(0) behind the ring's DMAs.
+      const int gi = __builtin_amdgcn_readfirstlane(grp0 + 2 * ch);
+      const uint32_t gw = reinterpret_cast<const uint32_t*>(a.grp)[gi >> 1];
+      int g0 = (int16_t)(gw & 0xffffu), g1 = (int16_t)(gw >> 16);
+      g0 = g0 < 0 ? g_safe : g0;
+      g1 = g1 < 0 ? g_safe : g1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        int g = a.grp[grp0 + 2 * ch + (bc[i] >> 1)];
-        g = g < 0 ? g_safe : g;
-        dma16(Bp + boff[i] + 16 * g + 8 * (bc[i] & 1), X + 1024 + 64 * (4 * wave + i));
+        const int g = (bc[i] >> 1) ? g1 : g0;
+        dma16_asm(Bp + boff[i] + 16 * g + 8 * (bc[i] & 1),
+                  lds_addr(X + 1024 + 64 * (4 * wave + i)));
       }
     };
-    auto compute_t = [&](const uint4* X) {
+    uint4 ta[2], tb[8];
+    auto read_t = [&](const uint4* X, int kk, uint4 (&av)[2], uint4 (&bv)[8]) {
+      const int c = 2 * kk + fk;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) av[j] = X[1024 + swz4(64 * wave + 32 * j + fr, c)];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) bv[i] = X[swz4(32 * i + fr, c)];
+    };
+    // Chunk ch: step 0 reads step 1's fragments and issues chunk ch+2 into
+    // Pv; the wait + barrier sit between the steps; step 1 reads the next
+    // chunk's step-0 fragments.
+    auto body_t = [&](int ch, const uint4* C, const uint4* Nx, const uint4* Pv) {
+      const int nc = ch + 2 < chunks32 ? ch + 2 : chunks32 - 1;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const int c = 2 * kk + fk;
-        uint4 wa[2], xb[8];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) wa[j] = X[1024 + swz4(64 * wave + 32 * j + fr, c)];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xb[i] = X[swz4(32 * i + fr, c)];
+        uint4 an[2], bn[8];
+        if (kk == 0) {
+          issue_t(nc, Pv);
+          read_t(C, 1, an, bn);
+        } else {
+          read_t(Nx, 0, an, bn);
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8_t, wa[j]), __builtin_bit_cast(bf16x8_t, xb[i]),
+                __builtin_bit_cast(bf16x8_t, ta[j]), __builtin_bit_cast(bf16x8_t, tb[i]),
                 acc[j][i], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 10; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kk == 0) {
+          ring_wait<8>();                       // chunk ch+1 landed, ch done
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) ta[j] = an[j];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) tb[i] = bn[i];
       }
     };
-    auto step_t = [&](int ch, uint4* Xc, uint4* Xn) {
-      __builtin_amdgcn_s_waitcnt(vm_wait(8));   // chunk ch done
-      ring_barrier();
-      issue_t(ch + 2 < chunks32 ? ch + 2 : chunks32 - 1, Xn);
-      if (ch < chunks32) compute_t(Xc);
-    };
-    // every wave is past its last base-stage read before the ring is reused
-    ring_barrier();
-    issue_t(0, sX0);
-    issue_t(chunks32 > 1 ? 1 : 0, sX1);
-    for (int ch = 0; ch < chunks32; ch += 3) {
-      step_t(ch, sX0, sX2);
-      step_t(ch + 1, sX1, sX0);
-      step_t(ch + 2, sX2, sX1);
+    issue_t(0, st0);
+    issue_t(chunks32 > 1 ? 1 : 0, st1);
+    ring_wait<8>();
+    read_t(st0, 0, ta, tb);
+    int ch = 0;
+    for (; ch + 3 <= chunks32; ch += 3) {
+      body_t(ch, st0, st1, st2);
+      body_t(ch + 1, st1, st2, st0);
+      body_t(ch + 2, st2, st0, st1);
     }
-    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    if (chunks32 - ch >= 1) body_t(ch, st0, st1, st2);
+    if (chunks32 - ch == 2) body_t(ch + 1, st1, st2, st0);
+    ring_wait<0>();
   }
 
-  // Epilogue: D[n][m] per tile -> 4 consecutive n per register quad.
+  // Epilogue through LDS: each wave converts its 64 columns x 128 rows at a
+  // time to bf16 in its own 16 KB region (rows of 128 B, chunks swizzled by
+  // (row >> 1) & 7 so both the 8-B writes and the 16-B reads are
+  // conflict-free), then stores whole 128-B row segments, 8 rows per
+  // instruction. Only the wave itself touches its region, and LDS accesses
+  // of one wave complete in order, so no barrier is needed inside.
+  uint4* const E = (wave < 2 ? st0 : st1) + 1024 * (wave & 1);
+  const bool st16 = (a.ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int h = 0; h < 2; ++h) {
+    uint2* const E2 = reinterpret_cast<uint2*>(E);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int m = m0 + 32 * i + fr;
+    for (int ii = 0; ii < 4; ++ii) {
+      const int i = 4 * h + ii;
+      const int ml = 32 * ii + fr;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + 64 * wave + 32 * j + 8 * q + 4 * fk;
-        if (m < a.M && n < a.N) {
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = 4 * j + q;
           uint2 v;
-          v.x = pack_bf16x2(acc[j][i][4 * q + 0], acc[j][i][4 * q + 1]);
-          v.y = pack_bf16x2(acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
-          *reinterpret_cast<uint2*>(a.y + (long long)m * a.ldy + n) = v;
+          v.x = pack_bf16x2_rne(acc[j][i][4 * q + 0], acc[j][i][4 * q + 1]);
+          v.y = pack_bf16x2_rne(acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
+          E2[ml * 16 + 2 * (c ^ ((ml >> 1) & 7)) + fk] = v;
+        }
+    }
+    const int cl = lane & 7;
+    const int n = n0 + 64 * wave + 8 * cl;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ml = 8 * r + (lane >> 3);
+      const uint4 v = E[ml * 8 + (cl ^ ((ml >> 1) & 7))];
+      const int m = m0 + 128 * h + ml;
+      if (m < a.M && n < a.N) {
+        uint16_t* yp = a.y + (long long)m * a.ldy + n;
+        if (st16) {
+          *reinterpret_cast<uint4*>(yp) = v;
+        } else {
+          reinterpret_cast<uint2*>(yp)[0] = make_uint2(v.x, v.y);
+          reinterpret_cast<uint2*>(yp)[1] = make_uint2(v.z, v.w);
         }
       }
     }
