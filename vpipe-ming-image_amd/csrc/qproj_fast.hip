@@ -61,11 +61,8 @@ constexpr unsigned vm_wait(unsigned v) {
 __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, 0);
 }
-__device__ __forceinline__ void dma4(const void* src, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_wave_base, 4, 0, 0);
-}
 
-// The same DMA written as inline asm, for rings whose waits are all
+// The DMA written as inline asm, for rings whose waits are all
 // explicit: the compiler then sees no LDS store it must order reads
 // against, so it cannot add a drain of its own (its alias tracking of LDS
 // DMA gives up at loop joins and would wait for vmcnt(0)). M0 carries the
@@ -74,13 +71,16 @@ __device__ __forceinline__ void dma4(const void* src, void* lds_wave_base) {
 // also orders every LDS access against the DMAs through its memory clobber.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16_asm(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(src), "s"(lds) : "m0");
+// Scalar-base form: address = 64-bit wave-uniform base (SGPRs) + 32-bit
+// per-lane byte offset, so advancing a stage is a scalar add and the issue
+// needs no VALU address arithmetic.
+__device__ __forceinline__ void dma16_sb(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "s"(lds) : "m0");
 }
-__device__ __forceinline__ void dma4_asm(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :: "v"(src), "s"(lds) : "m0");
+__device__ __forceinline__ void dma4_sb(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(off), "s"(base), "s"(lds) : "m0");
 }
 #pragma clang diagnostic pop
 
@@ -200,7 +200,9 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 
   // DMA sources for this lane, per stage (advance by k).
   // x tile: wave issues chunks q = 8*wave + i; lane p = 64q + lane.
-  long long xoff[8];
+  // Byte offsets from the stage's base (the host keeps every tile inside
+  // 4 GiB of its base, so they fit 32 bits).
+  uint32_t xoff[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int p = 64 * (8 * wave + i) + lane;
@@ -208,10 +210,10 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     const int c = (p & 7) ^ ((row >> 1) & 7);
     int m = m0 + row;
     m = m < mlast ? m : mlast;
-    xoff[i] = (long long)m * a.ldx + 8 * c;
+    xoff[i] = (uint32_t)(((long long)m * a.ldx + 8 * c) * 2);
   }
   // code tile: LDS chunk p holds row p / CPR, logical chunk (p % CPR) ^ sw
-  long long woff[WDMA];
+  uint32_t woff[WDMA];
 #pragma unroll
   for (int i = 0; i < WDMA; ++i) {
     const int p = 64 * (WDMA * wave + i) + lane;
@@ -219,25 +221,27 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     const int h = (p % CPR) ^ wswz<CPR>(r);
     int n = n0 + r;
     n = n < nlast ? n : nlast;
-    woff[i] = (long long)n * CPR + h;
+    woff[i] = (uint32_t)((n * CPR + h) * 16);
   }
   int sn = n0 + 64 * wave + lane;
   sn = sn < nlast ? sn : nlast;
+  const uint32_t soff = (uint32_t)sn * 4u;
 
   // The stage's DMAs in three groups (x rows 0-127, x rows 128-255, codes +
   // (s, b)), issued one group per k16 step of the stage before.
   auto issue_grp = [&](int g, int kt, const uint4* B) {
     if (g < 2) {
+      const void* base = x16 + (long long)kt * BK;
 #pragma unroll
       for (int i = 4 * g; i < 4 * g + 4; ++i)
-        dma16_asm(x16 + xoff[i] + kt * BK, lds_addr(B + 64 * (8 * wave + i)));
+        dma16_sb(base, xoff[i], lds_addr(B + 64 * (8 * wave + i)));
     } else {
+      const void* wbase = codes + (long long)kt * a.N * CPR;
 #pragma unroll
       for (int i = 0; i < WDMA; ++i)
-        dma16_asm(codes + (long long)kt * a.N * CPR + woff[i],
-                  lds_addr(B + BM * 8 + 64 * (WDMA * wave + i)));
-      dma4_asm(a.sb + (long long)kt * a.N + sn,
-               lds_addr(reinterpret_cast<const uint32_t*>(B + BM * 8 + WCH) + 64 * wave));
+        dma16_sb(wbase, woff[i], lds_addr(B + BM * 8 + 64 * (WDMA * wave + i)));
+      dma4_sb(a.sb + (long long)kt * a.N, soff,
+              lds_addr(reinterpret_cast<const uint32_t*>(B + BM * 8 + WCH) + 64 * wave));
     }
   };
 
@@ -408,8 +412,8 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     // groups (their T columns are exactly 0)
     const int g_safe =
         (int16_t)(reinterpret_cast<const uint32_t*>(a.grp)[grp0 >> 1] & 0xffffu);
-    long long toff[4];
-    long long boff[4];
+    uint32_t toff[4];
+    uint32_t boff[4];
     int bc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -418,10 +422,10 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
       const int c = (p & 3) ^ ((row >> 2) & 3);
       int m = m0 + row;
       m = m < mlast ? m : mlast;
-      toff[i] = (long long)m * a.ldt + t_col0 + 8 * c;
+      toff[i] = (uint32_t)(((long long)m * a.ldt + t_col0 + 8 * c) * 2);
       int n = n0 + row;
       n = n < seg_ne - 1 ? n : seg_ne - 1;
-      boff[i] = (long long)(n - seg_nb) * ldb;
+      boff[i] = (uint32_t)(((long long)(n - seg_nb) * ldb + 8 * (c & 1)) * 2);
       bc[i] = c;
     }
     // T region = first 16 KB of the stage buffer, B region = second. The
@@ -429,7 +433,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     auto issue_t = [&](int ch, const uint4* X) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        dma16_asm(a.t + toff[i] + 32 * ch, lds_addr(X + 64 * (4 * wave + i)));
+        dma16_sb(a.t + 32 * ch, toff[i], lds_addr(X + 64 * (4 * wave + i)));
       // The chunk's two groups are one aligned dword of the table (a
       // segment's groups start at a multiple of 4): a wave-uniform scalar
       // load (lgkmcnt), never a VMEM load the compiler would wait for with
@@ -442,8 +446,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int g = (bc[i] >> 1) ? g1 : g0;
-        dma16_asm(Bp + boff[i] + 16 * g + 8 * (bc[i] & 1),
-                  lds_addr(X + 1024 + 64 * (4 * wave + i)));
+        dma16_sb(Bp, boff[i] + (uint32_t)g * 32u, lds_addr(X + 1024 + 64 * (4 * wave + i)));
       }
     };
     uint4 ta[2], tb[8];

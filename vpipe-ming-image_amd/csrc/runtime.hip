@@ -769,7 +769,15 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
              "lora_xa launch");
     c->eng.lora_xa += 1;
   }
-  const bool fast = q->bits != 16 && q->fast && c->route != MING_ROUTE_GENERAL;
+  // The fast route addresses each operand as a 64-bit base plus 32-bit
+  // byte offsets: x (fp16 copy, row stride K), T and every B stack must fit.
+  bool fits32 = (uint64_t)M * (uint64_t)q->K * 2 <= (1ull << 32) &&
+                (uint64_t)M * (uint64_t)t_cols * 2 <= (1ull << 32);
+  for (int si = 0; si < nseg && t_cols > 0; ++si)
+    if (qa.seg[si].chunks > 0 &&
+        (uint64_t)q->segs[si].N * (uint64_t)q->b_ld[si] * 2 > (1ull << 32))
+      fits32 = false;
+  const bool fast = q->bits != 16 && q->fast && c->route != MING_ROUTE_GENERAL && fits32;
   qa.x = x; qa.ldx = ldx; qa.codes = q->codes_t; qa.sb = q->sb; qa.w16 = q->w16;
   qa.y = y; qa.ldy = ldy; qa.M = M; qa.N = q->N; qa.K = q->K;
   qa.t = T; qa.ldt = t_cols > 0 ? t_cols : 0; qa.nseg = nseg;
