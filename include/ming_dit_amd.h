@@ -185,6 +185,17 @@ int ming_qk_norm_rope(ming_ctx* ctx, uint16_t* x, int64_t ld, int q_col,
                       const uint16_t* wq, const uint16_t* wk,
                       const float* cos_t, const float* sin_t, float eps);
 
+/* Dense bidirectional attention (run_attn, ming-dit.cc:1905-2039, with the
+ * head-major transposes around it, 2085-2092): for every head h,
+ *   out[:, 128h + d] = softmax(scale * Q_h K_h^T) V_h,
+ * Q_h = qkv[:, q_col + 128h ...], K_h and V_h likewise at k_col / v_col, all
+ * token-major with row stride ld; out token-major with stride ldo. head_dim
+ * must be 128; strides and columns multiples of 8, pointers 16-byte
+ * aligned. No mask: every row attends to all `rows` keys. */
+int ming_attention(ming_ctx* ctx, const uint16_t* qkv, int64_t ld, int q_col,
+                   int k_col, int v_col, uint16_t* out, int64_t ldo, int rows,
+                   int n_heads, int head_dim, float scale);
+
 /* ---- block glue (ming_ops.metal; ming-dit.cc:1772-1884) -----------------------
  * All bf16, token-major, element strides; widths and strides multiples of
  * 8 and pointers 16-byte aligned where noted. */

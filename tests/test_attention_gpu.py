@@ -1,0 +1,143 @@
+"""Attention on the GPU against the f64 oracle (ming-dit.cc:1905-2039: dense,
+bidirectional, maskless, scale 1/sqrt(128), head dim 128).
+
+The kernel rounds P to bf16 before P.V (as the reference's steel kernel
+feeds P in the input type) and the output to bf16, so it is held to a
+rel-L2 of 6e-3 against the f64 oracle (whose output is bf16 too); bf16
+output rounding alone accounts for ~1.5e-3.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import bf16, f32, randn, to_dev, from_dev, empty_bf16, sync
+
+pytestmark = pytest.mark.gpu
+TOL = 6e-3
+
+
+def qkv_problem(seed, rows, heads, qscale=1.0, pad_cols=0):
+    w = heads * 128
+    q = bf16(randn(seed, (rows, w), qscale))
+    k = bf16(randn(seed + 1, (rows, w)))
+    v = bf16(randn(seed + 2, (rows, w)))
+    ld = 3 * w + pad_cols
+    qkv = np.zeros((rows, ld), np.uint16)
+    qkv[:, :w] = q
+    qkv[:, w:2 * w] = k
+    qkv[:, 2 * w:3 * w] = v
+    return qkv, q, k, v
+
+
+def run(ctx, qkv, rows, heads, q_col=None, k_col=None, v_col=None, ldo=None,
+        scale=None):
+    w = heads * 128
+    ld = qkv.shape[1]
+    q_col = 0 if q_col is None else q_col
+    k_col = w if k_col is None else k_col
+    v_col = 2 * w if v_col is None else v_col
+    ldo = ldo or w
+    d = to_dev(qkv)
+    out = empty_bf16(rows, ldo)
+    sync()
+    ctx.attention(d, ld, q_col, k_col, v_col, out, ldo, rows, heads, scale)
+    ctx.synchronize()
+    return from_dev(out)[:, :w]
+
+
+@pytest.mark.parametrize("rows,heads", [(64, 1), (37, 2), (128, 2), (200, 2),
+                                        (333, 3), (1000, 1), (256, 30)])
+def test_attention_matches_oracle(ctx, rows, heads):
+    qkv, q, k, v = qkv_problem(100 + rows, rows, heads)
+    got = run(ctx, qkv, rows, heads)
+    ref = orc.attention(q, k, v, heads, 128)
+    err = orc.rel_l2(f32(got), f32(ref))
+    assert err <= TOL, f"rows={rows} heads={heads}: rel-L2 {err:.3e}"
+
+
+def test_attention_peaked_softmax(ctx):
+    """Large logits (|s| ~ 40): the running max must rescale correctly."""
+    rows, heads = 500, 2
+    qkv, q, k, v = qkv_problem(7, rows, heads, qscale=4.0)
+    got = run(ctx, qkv, rows, heads)
+    ref = orc.attention(q, k, v, heads, 128)
+    assert orc.rel_l2(f32(got), f32(ref)) <= TOL
+
+
+def test_attention_identical_keys_average_values(ctx):
+    """All keys equal -> uniform weights -> every output row is mean(V)."""
+    rows, heads = 150, 1
+    qkv, q, k, v = qkv_problem(9, rows, heads)
+    qkv[:, 128:256] = qkv[0, 128:256]
+    got = f32(run(ctx, qkv, rows, heads))
+    mean = f32(v).astype(np.float64).mean(axis=0)
+    assert np.max(np.abs(got - mean[None, :])) <= 2e-2 * np.max(np.abs(mean)) + 2e-3
+
+
+def test_attention_strided_columns_and_output(ctx):
+    """q/k/v at shuffled column offsets inside a wider row; output stride > width."""
+    rows, heads = 190, 2
+    w = heads * 128
+    qkv, q, k, v = qkv_problem(11, rows, heads, pad_cols=64)
+    # layout [v | q | k | pad] instead of [q | k | v]
+    shuffled = np.zeros_like(qkv)
+    shuffled[:, :w] = v
+    shuffled[:, w:2 * w] = q
+    shuffled[:, 2 * w:3 * w] = k
+    got = run(ctx, shuffled, rows, heads, q_col=w, k_col=2 * w, v_col=0,
+              ldo=w + 40)
+    ref = orc.attention(q, k, v, heads, 128)
+    assert orc.rel_l2(f32(got), f32(ref)) <= TOL
+
+
+def test_attention_scale_argument(ctx):
+    rows, heads = 96, 1
+    qkv, q, k, v = qkv_problem(13, rows, heads)
+    got = run(ctx, qkv, rows, heads, scale=0.02)
+    ref = orc.attention(q, k, v, heads, 128, scale=0.02)
+    assert orc.rel_l2(f32(got), f32(ref)) <= TOL
+
+
+def test_attention_deterministic(ctx):
+    rows, heads = 300, 2
+    qkv, *_ = qkv_problem(15, rows, heads)
+    a = run(ctx, qkv, rows, heads)
+    b = run(ctx, qkv, rows, heads)
+    assert np.array_equal(a, b)
+
+
+def test_attention_full_length_one_head(ctx):
+    """Config 3's joint length (4352 = 4096 image + 256 text) on one head,
+    against the oracle (the other 29 heads are the same kernel path)."""
+    rows, heads = 4352, 1
+    qkv, q, k, v = qkv_problem(17, rows, heads)
+    got = run(ctx, qkv, rows, heads)
+    ref = orc.attention(q, k, v, heads, 128)
+    assert orc.rel_l2(f32(got), f32(ref)) <= TOL
+
+
+def test_attention_full_size_properties(ctx):
+    """30 heads x 4352 rows: every output finite and bounded by max|V|
+    (a convex combination of V rows per head)."""
+    rows, heads = 4352, 30
+    qkv, q, k, v = qkv_problem(19, rows, heads)
+    got = f32(run(ctx, qkv, rows, heads))
+    assert np.all(np.isfinite(got))
+    vmax = np.abs(f32(v)).reshape(rows, heads, 128).max(axis=0)   # [heads, 128]
+    g = np.abs(got).reshape(rows, heads, 128)
+    assert np.all(g <= vmax[None] * (1 + 2 ** -7) + 1e-6)
+
+
+def test_attention_rejects_bad_shapes(ctx):
+    import ming_dit_amd as m
+    rows, heads = 64, 1
+    qkv, *_ = qkv_problem(21, rows, heads)
+    d = to_dev(qkv)
+    out = empty_bf16(rows, 128)
+    with pytest.raises(m.MingError):
+        ctx.attention(d, qkv.shape[1], 0, 128, 256, out, 128, rows, heads,
+                      head_dim=64)
+    with pytest.raises(m.MingError):
+        ctx.attention(d, qkv.shape[1], 4, 128, 256, out, 128, rows, heads)
+    with pytest.raises(m.MingError):
+        ctx.attention(d, qkv.shape[1], 0, 128, 300, out, 128, rows, heads)

@@ -1,0 +1,300 @@
+// Dense bidirectional attention for the DiT blocks on MI355X (gfx950):
+// head dim 128, no mask, any sequence length (the ragged last key block is
+// masked out of the softmax, as the reference's unaligned specialization
+// does, ming-dit.cc:1905-1915).
+//
+// Operands stay where the block's projections put them: Q and K are read
+// token-major straight from the fused qkv output (head h at column +128h),
+// and the output is written token-major, so no head-major transpose of Q,
+// K or O exists. Only V is transposed (vt_transpose_kernel) into
+// V^T [head][d][key], keys contiguous and zero-padded to a multiple of 64.
+//
+// Per block: 4 waves x 32 queries = 128 queries of one head; keys in steps
+// of 64 through a two-stage LDS ring filled by direct global->LDS DMA.
+// Per step and wave:
+//   S^T = K . Q^T   2 key tiles x 8 d-slices of v_mfma_f32_32x32x16_bf16.
+//                   Each lane owns ONE query (the MFMA's column), so the
+//                   softmax row reductions are in-lane plus one exchange
+//                   with the other lane half. The K rows of every 16-key
+//                   slice are fed in the order {0-3, 8-11, 4-7, 12-15}
+//                   (bits 2 and 3 of the row swapped), which leaves lane
+//                   half h holding keys 8h..8h+7 of each slice in
+//                   consecutive registers -- exactly the B operand layout
+//                   of the P.V MFMA, so P never leaves registers.
+//   online softmax  exp2 domain (logits pre-multiplied by scale*log2 e),
+//                   running max exchanged across lane halves, running
+//                   sums kept per lane half and combined at the end.
+//   O^T += V^T.P^T  4 d-tiles x 4 key slices, P rounded to bf16 (the
+//                   reference's steel kernel also feeds P as the input
+//                   type to its second GEMM). V^T rows are fed in the same
+//                   swapped order, so each lane ends holding 8 consecutive
+//                   d of its query: 16-byte token-major stores.
+#include "common.h"
+#include "kernels.h"
+
+namespace ming {
+namespace {
+
+constexpr int ABQ = 128, ABK = 64, AHD = 128;
+
+__device__ __forceinline__ int swap23(int i) {
+  return (i & ~12) | ((i >> 2) & 1) << 3 | ((i >> 3) & 1) << 2;
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void adma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "s"(lds) : "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t alds(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// vmcnt(0) + LDS reads done + workgroup barrier (the DMAs are inline asm,
+// so every wait on them is explicit).
+__device__ __forceinline__ void attn_sync() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ float xor32(float v) {
+  return __shfl_xor(v, 32, 64);
+}
+
+__global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
+  // stage = K tile [64 keys][128 d] (16-B chunk c of row r at
+  // 16r + (c ^ (r & 15))) + V^T tile [128 d][64 keys] (swz8 rows of 128 B)
+  __shared__ uint4 sk0[1024], sv0[1024], sk1[1024], sv1[1024];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 31, fh = lane >> 5;
+  const int q0 = blockIdx.x * ABQ;
+  const int head = blockIdx.y;
+  const int R = a.R;
+  const int NKB = (R + ABK - 1) / ABK;
+
+  // Q^T fragments (B operand): lane = query fr, d = 16s + 8fh + 0..7
+  int qr = q0 + 32 * wave + fr;
+  qr = qr < R ? qr : R - 1;
+  uint4 qf[8];
+  {
+    const uint16_t* qp = a.q + (long long)qr * a.ldq + head * AHD + 8 * fh;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const uint4*>(qp + 16 * s);
+  }
+
+  // DMA offsets (bytes from the step's base). K: chunk p -> row p >> 4,
+  // logical chunk (p & 15) ^ (row & 15). V^T: chunk p -> row p >> 3,
+  // logical chunk (p & 7) ^ ((row >> 1) & 7).
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = 64 * (4 * wave + i) + lane;
+    const int kr = p >> 4;
+    const int kc = (p & 15) ^ (kr & 15);
+    // R < 64: one block, loaded from row 0; rows past R re-read row R-1
+    const int krow = R < ABK ? (kr < R ? kr : R - 1) : kr;
+    koff[i] = (uint32_t)(krow * a.ldk * 2 + kc * 16);
+    const int vr = p >> 3;
+    const int vc = (p & 7) ^ ((vr >> 1) & 7);
+    voff[i] = (uint32_t)(vr * a.ldv * 2 + vc * 16);
+  }
+  const uint16_t* kbase0 = a.k + head * AHD;
+  const uint16_t* vbase0 = a.vt + (long long)head * AHD * a.ldv;
+  // The last key block reads rows up to 63 past its start: clamp the block
+  // start so K rows stay inside [0, R) (the masked keys re-read valid rows).
+  auto issue = [&](int kb, uint4* SK, uint4* SV) {
+    int kstart = kb * ABK;
+    const int kmax = R - ABK;
+    const int kclamp = kstart < kmax ? kstart : (kmax > 0 ? kmax : 0);
+    const uint16_t* kb_base = kbase0 + (long long)kclamp * a.ldk;
+    const uint16_t* vb_base = vbase0 + kstart;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) adma16(kb_base, koff[i], alds(SK + 64 * (4 * wave + i)));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) adma16(vb_base, voff[i], alds(SV + 64 * (4 * wave + i)));
+  };
+
+  floatx16_t oacc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[u][r] = 0.0f;
+  float mrun = -INFINITY, lrun = 0.0f;
+  const float sl2 = a.sl2;
+
+  auto step = [&](int kb, const uint4* SK, const uint4* SV) {
+    // When R < 64 the (single) block was loaded from row 0; otherwise the
+    // last block was shifted back to R - 64: keys are then offset.
+    const int kstart = kb * ABK;
+    const int kmax = R - ABK;
+    const int kload = kstart < kmax ? kstart : (kmax > 0 ? kmax : 0);
+    const int shift = kstart - kload;      // 0 except for a shifted last block
+    floatx16_t sacc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[t][r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = 32 * t + swap23(fr) + shift;   // K row in the loaded tile
+      const int rr = row < ABK ? row : ABK - 1;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const uint4 kf = SK[16 * rr + ((2 * s + fh) ^ (rr & 15))];
+        sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, kf), __builtin_bit_cast(bf16x8_t, qf[s]),
+            sacc[t], 0, 0, 0);
+      }
+    }
+    // register r of tile t holds key 32t + 16(r/8) + 8fh + (r%8)
+    const bool tail = kstart + ABK > R;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = sacc[t][r] * sl2;
+        if (tail) {
+          const int key = kstart + 32 * t + 16 * (r >> 3) + 8 * fh + (r & 7);
+          x = key < R ? x : -INFINITY;
+        }
+        sacc[t][r] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = fmaxf(mloc, xor32(mloc));
+    const float mnew = fmaxf(mrun, mloc);
+    const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+    mrun = mnew;
+    float psum = 0.0f;
+    uint4 pf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = j >> 1, r0 = 8 * (j & 1);
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(sacc[t][r0 + e] - mnew);
+        psum += p[e];
+      }
+      pf[j].x = pack_bf16x2_rne(p[0], p[1]);
+      pf[j].y = pack_bf16x2_rne(p[2], p[3]);
+      pf[j].z = pack_bf16x2_rne(p[4], p[5]);
+      pf[j].w = pack_bf16x2_rne(p[6], p[7]);
+    }
+    lrun = lrun * alpha + psum;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[u][r] *= alpha;
+    // O^T[d][q] += V^T[d][k] P^T[k][q]; V^T row fed for output row i is
+    // d = 32u + swap23(i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int vrow = 32 * u + swap23(fr);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 vf = SV[vrow * 8 + ((2 * j + fh) ^ ((vrow >> 1) & 7))];
+        oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, vf), __builtin_bit_cast(bf16x8_t, pf[j]),
+            oacc[u], 0, 0, 0);
+      }
+    }
+  };
+
+  issue(0, sk0, sv0);
+  for (int kb = 0; kb < NKB; kb += 2) {
+    attn_sync();                                   // stage kb landed; sk1/sv1 free
+    issue(kb + 1 < NKB ? kb + 1 : NKB - 1, sk1, sv1);
+    step(kb, sk0, sv0);
+    if (kb + 1 >= NKB) break;
+    attn_sync();
+    issue(kb + 2 < NKB ? kb + 2 : NKB - 1, sk0, sv0);
+    step(kb + 1, sk1, sv1);
+  }
+  attn_sync();                                     // no DMA outlives the block
+
+  const float ltot = lrun + xor32(lrun);
+  const float inv = 1.0f / ltot;
+  const int q = q0 + 32 * wave + fr;
+  if (q < R) {
+    uint16_t* op = a.o + (long long)q * a.ldo + head * AHD + 8 * fh;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        uint4 v;
+        v.x = pack_bf16x2_rne(oacc[u][8 * hh + 0] * inv, oacc[u][8 * hh + 1] * inv);
+        v.y = pack_bf16x2_rne(oacc[u][8 * hh + 2] * inv, oacc[u][8 * hh + 3] * inv);
+        v.z = pack_bf16x2_rne(oacc[u][8 * hh + 4] * inv, oacc[u][8 * hh + 5] * inv);
+        v.w = pack_bf16x2_rne(oacc[u][8 * hh + 6] * inv, oacc[u][8 * hh + 7] * inv);
+        *reinterpret_cast<uint4*>(op + 32 * u + 16 * hh) = v;
+      }
+  }
+}
+
+// V [R][head*128 + d] (token-major) -> V^T [head][d][key], keys padded with
+// zeros to ldv. One block transposes 64 keys x 64 d through LDS.
+__global__ __launch_bounds__(256) void vt_transpose_kernel(const uint16_t* v, long long ldv_in,
+                                                           uint16_t* vt, int ldv, int R) {
+  __shared__ uint16_t t[64][64 + 2];
+  const int k0 = blockIdx.x * 64;
+  const int head = blockIdx.y >> 1, d0 = (blockIdx.y & 1) * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i;          // 512 chunks of 8 d
+    const int key = c >> 3, dc = (c & 7) * 8;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (k0 + key < R)
+      val = *reinterpret_cast<const uint4*>(v + (long long)(k0 + key) * ldv_in + head * AHD + d0 + dc);
+    const uint16_t* e = reinterpret_cast<const uint16_t*>(&val);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[dc + j][key] = e[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i;          // 512 chunks of 8 keys
+    const int d = c >> 3, kc = (c & 7) * 8;
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = t[d][kc + j];
+    uint4 val;
+    val.x = e[0] | ((uint32_t)e[1] << 16);
+    val.y = e[2] | ((uint32_t)e[3] << 16);
+    val.z = e[4] | ((uint32_t)e[5] << 16);
+    val.w = e[6] | ((uint32_t)e[7] << 16);
+    *reinterpret_cast<uint4*>(vt + ((long long)head * AHD + d0 + d) * ldv + k0 + kc) = val;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_attention(const AttnArgs& a, const uint16_t* v, long long ldv_in,
+                            hipStream_t s) {
+  if (a.R <= 0 || a.NH <= 0) return hipSuccess;
+  const int kblocks = a.ldv / 64;
+  hipLaunchKernelGGL(vt_transpose_kernel, dim3(kblocks, 2 * a.NH), dim3(256), 0, s, v,
+                     ldv_in, const_cast<uint16_t*>(a.vt), a.ldv, a.R);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attention_kernel, dim3((a.R + ABQ - 1) / ABQ, a.NH), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t validate_attention_kernels() {
+  hipFuncAttributes fa;
+  const void* fns[] = {reinterpret_cast<const void*>(&attention_kernel),
+                       reinterpret_cast<const void*>(&vt_transpose_kernel)};
+  for (const void* f : fns) {
+    const hipError_t e = hipFuncGetAttributes(&fa, f);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace ming

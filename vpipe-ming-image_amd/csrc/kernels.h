@@ -53,6 +53,26 @@ struct QprojArgs {
 
 hipError_t launch_qproj(int bits, const QprojArgs& a, hipStream_t s);
 
+// Dense attention, head dim 128: O = softmax(scale * Q K^T) V per head.
+// q, k: token-major rows (head h at column 128h); vt: V^T [NH][128][ldv]
+// written by the launch from v (token-major), keys zero-padded to ldv (a
+// multiple of 64 >= R); o: token-major [R][NH*128]. sl2 = scale * log2(e).
+struct AttnArgs {
+  const uint16_t* q;
+  long long ldq;
+  const uint16_t* k;
+  long long ldk;
+  const uint16_t* vt;
+  int ldv;
+  uint16_t* o;
+  long long ldo;
+  int R, NH;
+  float sl2;
+};
+hipError_t launch_attention(const AttnArgs& a, const uint16_t* v, long long ldv_in,
+                            hipStream_t s);
+hipError_t validate_attention_kernels();
+
 // T[m][c] = bf16(coef[c/16] * sum_k x[m][k] A[row(c)][k]) for c < n_cols,
 // row(c) = 16*grp[c/16] + c%16 (grp -1: a zero column). A is [R][K] bf16.
 struct LoraXaArgs {

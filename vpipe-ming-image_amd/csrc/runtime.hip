@@ -8,6 +8,7 @@
 // all-zero call runs the base kernel alone and a lone slot computes the
 // same bits whichever slot index holds it.
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -63,6 +64,8 @@ struct ming_ctx {
   size_t scratch_bytes = 0;
   void* xh = nullptr;          // fp16 copy of the projection input
   size_t xh_bytes = 0;
+  void* vt = nullptr;          // V^T [heads][128][keys] for attention
+  size_t vt_bytes = 0;
   void* part = nullptr;        // split-K partials of the stacked x.A GEMM
   size_t part_bytes = 0;
   int route = MING_ROUTE_AUTO;
@@ -262,6 +265,19 @@ int ensure_xh(ming_ctx* c, size_t bytes) {
   return MING_OK;
 }
 
+int ensure_vt(ming_ctx* c, size_t bytes) {
+  if (bytes <= c->vt_bytes) return MING_OK;
+  MING_HIP(hipStreamSynchronize(c->stream), "scratch grow sync");
+  if (c->vt) (void)hipFree(c->vt);
+  c->vt = nullptr;
+  c->vt_bytes = 0;
+  size_t want = std::max(bytes, (size_t)1 << 20);
+  if (hipMalloc(&c->vt, want) != hipSuccess)
+    return fail(MING_ERR_ALLOC, "attention V^T scratch allocation failed");
+  c->vt_bytes = want;
+  return MING_OK;
+}
+
 // Copy `bytes` from host or device into a fresh device buffer.
 int upload(ming_ctx* c, void** dst, const void* src, size_t bytes,
            int src_on_device) {
@@ -321,6 +337,7 @@ int ming_ctx_create(int device, void* hip_stream, ming_ctx** out) {
   if (e == hipSuccess) e = ming::validate_norm_kernels();
   if (e == hipSuccess) e = ming::validate_elementwise_kernels();
   if (e == hipSuccess) e = ming::validate_qproj_fast_kernels();
+  if (e == hipSuccess) e = ming::validate_attention_kernels();
   if (e != hipSuccess)
     return fail(MING_ERR_KERNEL,
                 std::string("kernel validation failed on this device (the "
@@ -351,6 +368,7 @@ int ming_ctx_destroy(ming_ctx* c) {
   (void)hipStreamSynchronize(c->stream);
   if (c->scratch) (void)hipFree(c->scratch);
   if (c->xh) (void)hipFree(c->xh);
+  if (c->vt) (void)hipFree(c->vt);
   if (c->part) (void)hipFree(c->part);
   for (auto& rec : c->recs) {
     (void)hipEventDestroy(rec.a);
@@ -884,6 +902,44 @@ int ming_qk_norm_rope(ming_ctx* c, uint16_t* x, int64_t ld, int q_col, int k_col
                                                            sin_t, eps, c->stream); }),
            "qk_norm_rope launch");
   c->eng.qk_norm_rope += 1;
+  return ok();
+}
+
+int ming_attention(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int k_col,
+                   int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
+                   int head_dim, float scale) {
+  if (!c || !qkv || !out) return fail(MING_ERR_ARG, "ming_attention: null argument");
+  if (head_dim != 128)
+    return fail(MING_ERR_SHAPE, "ming_attention: head_dim must be 128");
+  const int64_t w = (int64_t)n_heads * 128;
+  if (rows < 0 || n_heads <= 0 || q_col < 0 || k_col < 0 || v_col < 0 || q_col % 8 ||
+      k_col % 8 || v_col % 8 || ld % 8 || ldo % 8 || q_col + w > ld || k_col + w > ld ||
+      v_col + w > ld || ldo < w)
+    return fail(MING_ERR_SHAPE, "ming_attention: bad columns or strides");
+  if (!aligned(qkv, 16) || !aligned(out, 16))
+    return fail(MING_ERR_ARG, "ming_attention: pointers must be 16-byte aligned");
+  if (!(scale > 0.0f) || !std::isfinite(scale))
+    return fail(MING_ERR_ARG, "ming_attention: scale must be positive and finite");
+  // the K tile DMA addresses 64 rows from a scalar base with 32-bit offsets
+  if ((uint64_t)ld * 2 * 64 >= (1ull << 31))
+    return fail(MING_ERR_SHAPE, "ming_attention: row stride too large");
+  if (rows == 0) return ok();
+  DeviceGuard g(c->device);
+  const int ldv = (rows + 63) / 64 * 64;
+  int rc = ensure_vt(c, (size_t)n_heads * 128 * ldv * 2);
+  if (rc != MING_OK) return rc;
+  ming::AttnArgs a{};
+  a.q = qkv + q_col; a.ldq = ld;
+  a.k = qkv + k_col; a.ldk = ld;
+  a.vt = (const uint16_t*)c->vt; a.ldv = ldv;
+  a.o = out; a.ldo = ldo;
+  a.R = rows; a.NH = n_heads;
+  a.sl2 = scale * 1.4426950408889634f;
+  const double flops = 4.0 * (double)rows * rows * 128.0 * n_heads;
+  MING_HIP(profiled(c, kBAttn, flops, 8.0 * rows * w,
+                    [&] { return ming::launch_attention(a, qkv + v_col, ld, c->stream); }),
+           "attention launch");
+  c->eng.attention += 1;
   return ok();
 }
 

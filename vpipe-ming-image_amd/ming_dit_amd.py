@@ -82,6 +82,8 @@ def lib():
         "ming_rmsnorm": ([vp, vp, i64, vp, vp, i64, i32, i32, f32], i32),
         "ming_rope_table": ([vp, vp, vp, vp, i32, C.POINTER(i32), i32,
                              C.c_double, vp, vp], i32),
+        "ming_attention": ([vp, vp, i64, i32, i32, i32, vp, i64, i32, i32, i32,
+                            f32], i32),
         "ming_qk_norm_rope": ([vp, vp, i64, i32, i32, i32, i32, i32, vp, vp,
                                vp, vp, f32], i32),
         "ming_ctx_set_profiling": ([vp, i32], i32),
@@ -216,6 +218,15 @@ class Ctx:
                                        n_heads, head_dim, _ptr(wq), _ptr(wk),
                                        _ptr(cos_t), _ptr(sin_t), eps))
 
+
+    def attention(self, qkv, ld: int, q_col: int, k_col: int, v_col: int,
+                  out, ldo: int, rows: int, n_heads: int, scale=None,
+                  head_dim: int = 128):
+        if scale is None:
+            scale = 1.0 / head_dim ** 0.5
+        _check(lib().ming_attention(self.h, _ptr(qkv), ld, q_col, k_col, v_col,
+                                    _ptr(out), ldo, rows, n_heads, head_dim,
+                                    float(scale)))
 
     def swiglu(self, g, u, out, rows: int, n: int, ldg=None, ldu=None,
                ldo=None):
