@@ -237,6 +237,106 @@ int ming_quantize_pack(ming_ctx* ctx, const float* w, int N, int K, int bits,
                        int group, uint32_t* codes, uint16_t* scales,
                        uint16_t* biases);
 
+/* ---- block and model drivers ------------------------------------------------------
+ * The reference's run_block, fill_mod and forward sequence (ming-dit.cc:2065-2273,
+ * 2266-2281, 1490-2563) over the entry points above. Everything is borrowed:
+ * weights, gains and biases stay owned by the caller and must outlive the
+ * block call / the model. Gains and biases are bf16 device vectors. */
+typedef struct ming_block_desc {
+  /* [out][in]: q, k, v, o [H][H]; w1, w3 [ffn][H]; w2 [H][ffn] */
+  const ming_qweight* q;
+  const ming_qweight* k;
+  const ming_qweight* v;
+  const ming_qweight* o;
+  const ming_qweight* w1;
+  const ming_qweight* w3;
+  const ming_qweight* w2;
+  /* adaLN_modulation [4H][adaln_dim] + bias [4H] on modulated blocks (noise
+   * refiner, layers); NULL on the context refiner, which is unmodulated */
+  const ming_qweight* ada;
+  const uint16_t* ada_b;
+  /* attention_norm1/2, ffn_norm1/2 [H]; q/k norms [head_dim] */
+  const uint16_t* an1;
+  const uint16_t* an2;
+  const uint16_t* fn1;
+  const uint16_t* fn2;
+  const uint16_t* nq;
+  const uint16_t* nk;
+} ming_block_desc;
+
+typedef struct ming_block_dims {
+  int hidden;      /* H; H / n_heads must be 128 */
+  int n_heads;
+  int ffn;
+  int adaln_dim;
+  float eps;       /* RMSNorm and qk-norm epsilon (1e-5) */
+} ming_block_dims;
+
+/* Workspace one ming_block_forward over `rows` rows needs (bytes). */
+size_t ming_block_workspace_bytes(const ming_block_dims* dims, int rows);
+/* One block, in place on x [rows][H] (row stride H): pre-norm (gain folded with
+ * the adaLN scale on modulated blocks), q/k/v, qk-norm + RoPE (tables cos_t /
+ * sin_t [rows][64] for these rows), attention, to_out, post-norm, gated (tanh)
+ * or plain residual; then the SwiGLU feed-forward the same way. temb [adaln_dim]
+ * is the adaLN input (modulated blocks only); scales are the 8 live strengths of
+ * the LoRA slots bound on the projections (NULL: none). */
+int ming_block_forward(ming_ctx* ctx, const ming_block_desc* b, const ming_block_dims* dims,
+                       uint16_t* x, int rows, const float* cos_t, const float* sin_t,
+                       const uint16_t* temb, const float* scales, void* ws,
+                       size_t ws_bytes);
+
+typedef struct ming_model ming_model;
+typedef struct ming_model_desc {
+  int hidden;        /* 3840 */
+  int n_heads;       /* 30 (head_dim 128) */
+  int ffn;           /* 10240 */
+  int n_layers;      /* 30 main layers */
+  int n_refiner;     /* 2 context-refiner and 2 noise-refiner blocks */
+  int adaln_dim;     /* 256 */
+  int time_freq;     /* 256 */
+  int time_mid;      /* 1024 */
+  int patch_dim;     /* 64 = patch^2 * in_channels */
+  int cap_dim;       /* 2560: caption features of the query rows */
+  float eps;         /* 1e-5 */
+  float rope_theta;  /* 256 */
+  float t_scale;     /* 1000 */
+  int axes[3];       /* rotary dims per axis (32, 48, 48) */
+  int axes_lens[3];  /* positions per axis must stay below these */
+  const ming_block_desc* ctx_blocks;  /* [n_refiner], unmodulated */
+  const ming_block_desc* blocks;      /* [n_refiner + n_layers]: noise refiner, layers */
+  const ming_qweight* time_1;         /* t_embedder.mlp.0 [time_mid][time_freq] */
+  const uint16_t* time_1b;
+  const ming_qweight* time_2;         /* t_embedder.mlp.2 [adaln_dim][time_mid] */
+  const uint16_t* time_2b;
+  const ming_qweight* x_in;           /* x_embedder [H][patch_dim] */
+  const uint16_t* x_in_b;
+  const uint16_t* cap_norm;           /* cap_embedder.0 RMSNorm [cap_dim] */
+  const ming_qweight* cap_in;         /* cap_embedder.1 [H][cap_dim] */
+  const uint16_t* cap_in_b;
+  const ming_qweight* final_ada;      /* final_layer.adaLN_modulation [H][adaln_dim] */
+  const uint16_t* final_ada_b;
+  const ming_qweight* final_lin;      /* final_layer.linear [patch_dim][H] */
+  const uint16_t* final_lin_b;
+} ming_model_desc;
+
+/* MingDit::load over in-memory weights: validates the dimensions and every
+ * weight's shape, refusing rather than degrading. */
+int ming_model_create(ming_ctx* ctx, const ming_model_desc* d, ming_model** out);
+int ming_model_destroy(ming_model* m);
+/* set_lora_scale / lora_scale (ming-dit.cc:3024-3039): live between forwards. */
+int ming_model_set_lora_scale(ming_model* m, int slot, float s);
+float ming_model_lora_scale(const ming_model* m, int slot);
+/* forward (ming-dit.cc:1490-2563): latents [img_tokens][patch_dim] and the
+ * caption [cap_len][cap_stride] (rows < query_rows carry cap_dim features for
+ * cap_embedder, the rest H-wide rows that bypass it) in device memory; the
+ * joint layout's positions (host int32 [img_tokens + cap_len] per axis, image
+ * rows first); out [img_tokens][patch_dim] device, the velocity before
+ * negation. Synchronous: returns after the GPU finished. */
+int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* cap,
+                       int64_t cap_stride, int img_tokens, int cap_len, int query_rows,
+                       const int32_t* pos_t, const int32_t* pos_h, const int32_t* pos_w,
+                       float sigma, uint16_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -343,3 +343,116 @@ def rel_l2(a, b) -> float:
     den = float(np.sqrt(np.sum(b * b)))
     num = float(np.sqrt(np.sum((a - b) ** 2)))
     return num / den if den > 0 else num
+
+
+# ---- block and model, composed from the pieces above ---------------------------
+# The reference's run_block (ming-dit.cc:2065-2263), fill_mod (2266-2273), time
+# MLP (2276-2281), embeddings (2283-2304) and final layer (2557-2563), with
+# bf16 values at the same boundaries as the library: each projection output,
+# norm output, modulation and residual is a bf16 plane.
+def lin(x_bf16, w, loras=None, scales=None) -> np.ndarray:
+    """One projection, rounded to bf16 once. w: {"codes","scales","biases",
+    "bits"} (a pack) or {"w": bf16 [N,K]}; loras: per slot (A, B, fold) or
+    None; scales: the 8 live strengths. A slot is live when bound and its
+    strength is non-zero (lora_for_ + Stack::add, ming-dit.cc:3007-3022);
+    its coefficient is fold * strength."""
+    live = []
+    if loras is not None and scales is not None:
+        for i, l in enumerate(loras):
+            if l is not None and float(scales[i]) != 0.0:
+                A, B, fold = l
+                live.append((A, B, np.float32(fold) * np.float32(scales[i])))
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    if "w" in w:
+        y = proj(x, bf16_to_f32(w["w"]), live)
+    else:
+        y = qproj_packed(x, w["codes"], w["scales"], w["biases"], w["bits"],
+                         live)
+    return f32_to_bf16(y)
+
+
+def residual_add(h_bf16, sub_bf16) -> np.ndarray:
+    """h = bf16(h + sub), the f32 sum rounded once (ming_ops.metal resid)."""
+    s = bf16_to_f32(h_bf16) + bf16_to_f32(sub_bf16)
+    return f32_to_bf16(s.astype(np.float32))
+
+
+def silu_bf16(x_bf16) -> np.ndarray:
+    """bf16(silu(x)) through the bias+silu path with a zero bias."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    return bias_act(x.reshape(1, -1), np.zeros(x.size, np.uint16),
+                    silu=True).reshape(x.shape)
+
+
+def block_forward(x_bf16, blk, n_heads, cos_t, sin_t, temb=None, scales=None,
+                  eps=1e-5) -> np.ndarray:
+    """One block. blk: "q","k","v","o","w1","w3","w2" weights (see lin),
+    "loras": {name: [8 x (A, B, fold) or None]}, gains "an1","an2","fn1",
+    "fn2" [H], "nq","nk" [128], and "ada" + "ada_b" on modulated blocks."""
+    x = np.array(x_bf16, np.uint16, copy=True, order="C")
+    rows, H = x.shape
+    L = blk.get("loras", {})
+
+    def P(name, inp):
+        return lin(inp, blk[name], L.get(name), scales)
+
+    modulated = blk.get("ada") is not None
+    g1, g3 = blk["an1"], blk["fn1"]
+    if modulated:
+        mods = bias_act(lin(np.asarray(temb, np.uint16).reshape(1, -1),
+                            blk["ada"]), blk["ada_b"])[0]
+        g1 = fold_gain(blk["an1"], mods[:H])
+        g3 = fold_gain(blk["fn1"], mods[2 * H:3 * H])
+    nrm = rmsnorm(x, g1, eps)
+    qkv = np.concatenate([P("q", nrm), P("k", nrm), P("v", nrm)], axis=1)
+    qkv = qk_norm_rope(qkv, 0, H, n_heads, 128, blk["nq"], blk["nk"], cos_t,
+                       sin_t, 0, eps)
+    ao = attention(qkv[:, :H], qkv[:, H:2 * H], qkv[:, 2 * H:], n_heads, 128)
+    ob = rmsnorm(P("o", ao), blk["an2"], eps)
+    if modulated:
+        x = gated_residual(x, mods[H:2 * H], ob)
+    else:
+        x = residual_add(x, ob)
+    nrm = rmsnorm(x, g3, eps)
+    a = swiglu(P("w1", nrm), P("w3", nrm))
+    ob = rmsnorm(P("w2", a), blk["fn2"], eps)
+    if modulated:
+        x = gated_residual(x, mods[3 * H:], ob)
+    else:
+        x = residual_add(x, ob)
+    return x
+
+
+def model_forward(m, latents, cap, img, cap_len, query_rows, pos_t, pos_h,
+                  pos_w, sigma, scales=None) -> np.ndarray:
+    """MingDit::forward. m: dims ("hidden","n_heads","n_refiner","cap_dim",
+    "time_freq","t_scale","rope_theta","axes","eps"), "ctx_blocks" and
+    "blocks" (block dicts), and the time / embedding / final-layer weights
+    and biases. Returns the velocity [img][patch_dim] (bf16)."""
+    H, NH, eps = m["hidden"], m["n_heads"], m.get("eps", 1e-5)
+    Q, JT = query_rows, img + cap_len
+    cos_t, sin_t = rope_table(pos_t, pos_h, pos_w, m["axes"], 128,
+                              m["rope_theta"])
+    tin = f32_to_bf16(time_proj(sigma, m["t_scale"], m["time_freq"]))
+    te1 = bias_act(lin(tin.reshape(1, -1), m["time_1"]), m["time_1b"],
+                   silu=True)
+    temb = bias_act(lin(te1, m["time_2"]), m["time_2b"])[0]
+    tsilu = silu_bf16(temb)
+    joint = np.zeros((JT, H), np.uint16)
+    joint[:img] = bias_act(lin(latents, m["x_in"]), m["x_in_b"])
+    if Q > 0:
+        capn = rmsnorm(np.ascontiguousarray(cap[:Q, :m["cap_dim"]]),
+                       m["cap_norm"], eps)
+        joint[img:img + Q] = bias_act(lin(capn, m["cap_in"]), m["cap_in_b"])
+    joint[img + Q:] = cap[Q:cap_len, :H]
+    for blk in m["ctx_blocks"]:
+        joint[img:] = block_forward(joint[img:], blk, NH, cos_t[img:],
+                                    sin_t[img:], None, scales, eps)
+    for i, blk in enumerate(m["blocks"]):
+        rows = img if i < m["n_refiner"] else JT
+        joint[:rows] = block_forward(joint[:rows], blk, NH, cos_t[:rows],
+                                     sin_t[:rows], temb, scales, eps)
+    outmod = bias_act(lin(tsilu.reshape(1, -1), m["final_ada"]),
+                      m["final_ada_b"])[0]
+    nrm = ln_modulate(joint[:img], outmod)
+    return bias_act(lin(nrm, m["final_lin"]), m["final_lin_b"])

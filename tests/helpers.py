@@ -69,3 +69,54 @@ def empty_bf16(*shape):
 def sync():
     import torch
     torch.cuda.synchronize()
+
+
+# ---- blocks and models (small dims for the oracle, GPU objects beside) ----------
+BLOCK_PROJS = ("q", "k", "v", "o", "w1", "w3", "w2")
+
+
+def block_proj_shapes(H, F):
+    return {"q": (H, H), "k": (H, H), "v": (H, H), "o": (H, H),
+            "w1": (F, H), "w3": (F, H), "w2": (H, F)}
+
+
+def build_block(ctx, seed, H, F, adaln, bits=4, modulated=True,
+                slots=((0, 4, 1.0), (3, 16, 0.5))):
+    """A random block as (oracle dict, gpu dict, BlockDesc). Weights ~ N(0, .02)
+    quantized by the oracle's packer; gains ~ 1 + N(0, .1); adaLN bias
+    ~ N(0, .1); LoRA (slot, rank, fold) bound on all seven projections. Every
+    tensor has a fixed seed of its own, so the same seed with other slots
+    gives the same base block."""
+    import ming_dit_amd as m
+    ob = {"loras": {}}
+    gp = {}
+    for i, (name, (N, K)) in enumerate(block_proj_shapes(H, F).items()):
+        pack, _ = make_weight(seed + 100 * i, N, K, bits)
+        ob[name] = dict(pack, bits=bits)
+        qw = m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
+                                 pack["biases"], bits)
+        lor = [None] * 8
+        for slot, rank, fold in slots:
+            A, B = make_lora(seed + 100 * i + 10 + 2 * slot, N, K, rank)
+            qw.bind_lora(slot, A, B, fold)
+            lor[slot] = (A, B, fold)
+        ob["loras"][name] = lor
+        gp[name] = qw
+    if modulated:
+        pack, _ = make_weight(seed + 1000, 4 * H, adaln, bits)
+        ob["ada"] = dict(pack, bits=bits)
+        gp["ada"] = m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
+                                        pack["biases"], bits)
+        ob["ada_b"] = bf16(randn(seed + 1001, (4 * H,), 0.1))
+        gp["ada_b"] = to_dev(ob["ada_b"])
+    for j, (g, n) in enumerate((("an1", H), ("an2", H), ("fn1", H),
+                                ("fn2", H), ("nq", 128), ("nk", 128))):
+        ob[g] = bf16(1.0 + randn(seed + 1002 + j, (n,), 0.1))
+        gp[g] = to_dev(ob[g])
+    return ob, gp, m.block_desc(**gp)
+
+
+def grid_positions(rows, width=16, t=257):
+    """Image-like rotary positions (t, row, col) for `rows` tokens."""
+    i = np.arange(rows, dtype=np.int32)
+    return (np.full(rows, t, np.int32), i // width, i % width)

@@ -17,6 +17,7 @@
 
 #include "../../include/ming_dit_amd.h"
 #include "kernels.h"
+#include "rt.h"
 
 namespace {
 
@@ -363,7 +364,7 @@ int ming_ctx_destroy(ming_ctx* c) {
   if (!c) return ok();
   if (c->live_weights > 0)
     return fail(MING_ERR_STATE,
-                "ming_ctx_destroy: destroy the context's weights first");
+                "ming_ctx_destroy: destroy the context's weights and models first");
   DeviceGuard g(c->device);
   (void)hipStreamSynchronize(c->stream);
   if (c->scratch) (void)hipFree(c->scratch);
@@ -1126,3 +1127,11 @@ int ming_quantize_pack(ming_ctx* c, const float* w, int N, int K, int bits,
 }
 
 }  // extern "C"
+
+namespace ming {
+int rt_fail(int code, const std::string& why) { return fail(code, why); }
+int rt_ok() { return ok(); }
+int rt_device(const ming_ctx* c) { return c ? c->device : -1; }
+void rt_retain(ming_ctx* c) { c->live_weights += 1; }
+void rt_release(ming_ctx* c) { c->live_weights -= 1; }
+}  // namespace ming

@@ -46,6 +46,34 @@ class ProfileBucket(C.Structure):
                 ("bytes", C.c_double)]
 
 
+class BlockDesc(C.Structure):
+    """ming_block_desc: borrowed weights (qweight handles) and bf16 gains."""
+    _fields_ = [(n, C.c_void_p) for n in
+                ("q", "k", "v", "o", "w1", "w3", "w2", "ada", "ada_b", "an1",
+                 "an2", "fn1", "fn2", "nq", "nk")]
+
+
+class BlockDims(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("n_heads", C.c_int), ("ffn", C.c_int),
+                ("adaln_dim", C.c_int), ("eps", C.c_float)]
+
+
+class ModelDesc(C.Structure):
+    _fields_ = ([(n, C.c_int) for n in
+                 ("hidden", "n_heads", "ffn", "n_layers", "n_refiner",
+                  "adaln_dim", "time_freq", "time_mid", "patch_dim",
+                  "cap_dim")]
+                + [("eps", C.c_float), ("rope_theta", C.c_float),
+                   ("t_scale", C.c_float), ("axes", C.c_int * 3),
+                   ("axes_lens", C.c_int * 3),
+                   ("ctx_blocks", C.POINTER(BlockDesc)),
+                   ("blocks", C.POINTER(BlockDesc))]
+                + [(n, C.c_void_p) for n in
+                   ("time_1", "time_1b", "time_2", "time_2b", "x_in",
+                    "x_in_b", "cap_norm", "cap_in", "cap_in_b", "final_ada",
+                    "final_ada_b", "final_lin", "final_lin_b")])
+
+
 def lib():
     """Load the built library (raises if it is not there)."""
     global _lib
@@ -99,6 +127,17 @@ def lib():
         "ming_silu": ([vp, vp, vp, i32], i32),
         "ming_ln_modulate": ([vp, vp, i64, vp, vp, i64, i32, i32, f32], i32),
         "ming_quantize_pack": ([vp, vp, i32, i32, i32, i32, vp, vp, vp], i32),
+        "ming_block_workspace_bytes": ([C.POINTER(BlockDims), i32], C.c_size_t),
+        "ming_block_forward": ([vp, C.POINTER(BlockDesc), C.POINTER(BlockDims),
+                                vp, i32, vp, vp, vp, C.POINTER(f32), vp,
+                                C.c_size_t], i32),
+        "ming_model_create": ([vp, C.POINTER(ModelDesc), C.POINTER(vp)], i32),
+        "ming_model_destroy": ([vp], i32),
+        "ming_model_set_lora_scale": ([vp, i32, f32], i32),
+        "ming_model_lora_scale": ([vp, i32], f32),
+        "ming_model_forward": ([vp, vp, vp, i64, i32, i32, i32,
+                                C.POINTER(C.c_int32), C.POINTER(C.c_int32),
+                                C.POINTER(C.c_int32), f32, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -228,6 +267,24 @@ class Ctx:
                                     _ptr(out), ldo, rows, n_heads, head_dim,
                                     float(scale)))
 
+    def block_forward(self, desc: "BlockDesc", dims: "BlockDims", x, rows: int,
+                      cos_t, sin_t, temb=None, scales=None, ws=None):
+        """ming_block_forward in place on x [rows][H]; ws (a device tensor
+        of at least block_workspace_bytes) is allocated here when None."""
+        need = self.block_workspace_bytes(dims, rows)
+        if ws is None:
+            import torch
+            ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        sc = _scales(scales) if scales is not None else None
+        _check(lib().ming_block_forward(self.h, C.byref(desc), C.byref(dims),
+                                        _ptr(x), rows, _ptr(cos_t), _ptr(sin_t),
+                                        _ptr(temb), sc, _ptr(ws), need))
+        return ws
+
+    @staticmethod
+    def block_workspace_bytes(dims: "BlockDims", rows: int) -> int:
+        return int(lib().ming_block_workspace_bytes(C.byref(dims), rows))
+
     def swiglu(self, g, u, out, rows: int, n: int, ldg=None, ldu=None,
                ldo=None):
         _check(lib().ming_swiglu(self.h, _ptr(g), ldg or n, _ptr(u), ldu or n,
@@ -323,6 +380,72 @@ class QWeight:
     def close(self):
         if self.h:
             lib().ming_qweight_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _h(obj) -> int | None:
+    """Handle (QWeight) or device pointer (tensor) or None, as an int."""
+    if obj is None:
+        return None
+    if isinstance(obj, QWeight):
+        return obj.h.value
+    return _ptr(obj)
+
+
+def block_desc(**parts) -> BlockDesc:
+    """BlockDesc from QWeights (q, k, v, o, w1, w3, w2, ada) and bf16 device
+    tensors (ada_b, an1, an2, fn1, fn2, nq, nk)."""
+    d = BlockDesc()
+    for name, _ in BlockDesc._fields_:
+        setattr(d, name, _h(parts.get(name)))
+    d._keep = dict(parts)      # the handles stay valid while the desc lives
+    return d
+
+
+class Model:
+    """ming_model over borrowed weights: the caller keeps every QWeight and
+    tensor in `desc` alive for the model's lifetime (held here too)."""
+
+    def __init__(self, ctx: Ctx, desc: ModelDesc, ctx_blocks, blocks,
+                 keep=()):
+        self.ctx = ctx
+        self._cb = (BlockDesc * max(len(ctx_blocks), 1))(*ctx_blocks)
+        self._mb = (BlockDesc * max(len(blocks), 1))(*blocks)
+        desc.ctx_blocks = C.cast(self._cb, C.POINTER(BlockDesc))
+        desc.blocks = C.cast(self._mb, C.POINTER(BlockDesc))
+        self.desc = desc
+        self._keep = list(keep)
+        h = C.c_void_p()
+        _check(lib().ming_model_create(ctx.h, C.byref(desc), C.byref(h)))
+        self.h = h
+        ctx._weights.add(self)
+
+    def set_lora_scale(self, slot: int, s: float):
+        _check(lib().ming_model_set_lora_scale(self.h, slot, float(s)))
+
+    def lora_scale(self, slot: int) -> float:
+        return float(lib().ming_model_lora_scale(self.h, slot))
+
+    def forward(self, latents, cap, cap_stride: int, img_tokens: int,
+                cap_len: int, query_rows: int, pos_t, pos_h, pos_w,
+                sigma: float, out):
+        import numpy as np
+        arrs = [np.ascontiguousarray(a, np.int32) for a in (pos_t, pos_h, pos_w)]
+        ptrs = [a.ctypes.data_as(C.POINTER(C.c_int32)) for a in arrs]
+        _check(lib().ming_model_forward(self.h, _ptr(latents), _ptr(cap),
+                                        cap_stride, img_tokens, cap_len,
+                                        query_rows, *ptrs, float(sigma),
+                                        _ptr(out)))
+
+    def close(self):
+        if self.h:
+            lib().ming_model_destroy(self.h)
             self.h = None
 
     def __del__(self):
