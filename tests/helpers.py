@@ -120,3 +120,56 @@ def grid_positions(rows, width=16, t=257):
     """Image-like rotary positions (t, row, col) for `rows` tokens."""
     i = np.arange(rows, dtype=np.int32)
     return (np.full(rows, t, np.int32), i // width, i % width)
+
+
+def build_model(ctx, seed, H=256, NH=2, F=512, n_layers=2, n_refiner=1,
+                adaln=64, time_freq=64, time_mid=128, patch_dim=64,
+                cap_dim=128, bits=4, slots=((0, 4, 1.0), (3, 16, 0.5))):
+    """A random model: (oracle dict for oracle.model_forward, Model). The
+    non-block weights are dense bf16, as the reference leaves them
+    (MingQuantFamily excludes the embedders and the final layer)."""
+    import ming_dit_amd as m
+    mo = {"hidden": H, "n_heads": NH, "n_refiner": n_refiner,
+          "cap_dim": cap_dim, "time_freq": time_freq, "t_scale": 1000.0,
+          "rope_theta": 256.0, "axes": (32, 48, 48), "eps": 1e-5}
+    keep = []
+    mo["ctx_blocks"], cb = [], []
+    for i in range(n_refiner):
+        ob, gp, d = build_block(ctx, seed + 10000 * (i + 1), H, F, adaln, bits,
+                                False, slots)
+        mo["ctx_blocks"].append(ob)
+        cb.append(d)
+        keep.append(gp)
+    mo["blocks"], mb = [], []
+    for i in range(n_refiner + n_layers):
+        ob, gp, d = build_block(ctx, seed + 10000 * (i + 11), H, F, adaln, bits,
+                                True, slots)
+        mo["blocks"].append(ob)
+        mb.append(d)
+        keep.append(gp)
+    dev = {}
+    for j, (name, N, K) in enumerate((("time_1", time_mid, time_freq),
+                                      ("time_2", adaln, time_mid),
+                                      ("x_in", H, patch_dim),
+                                      ("cap_in", H, cap_dim),
+                                      ("final_ada", H, adaln),
+                                      ("final_lin", patch_dim, H))):
+        pack, _ = make_weight(seed + 500 + 2 * j, N, K, 16, std=1.0 / np.sqrt(K))
+        mo[name] = pack
+        dev[name] = m.QWeight.dense(ctx, pack["w"])
+        b = bf16(randn(seed + 501 + 2 * j, (N,), 0.05))
+        mo[name + "b" if name.startswith("time") else name + "_b"] = b
+        dev[name + "b" if name.startswith("time") else name + "_b"] = to_dev(b)
+    mo["cap_norm"] = bf16(1.0 + randn(seed + 600, (cap_dim,), 0.1))
+    dev["cap_norm"] = to_dev(mo["cap_norm"])
+    d = m.ModelDesc()
+    d.hidden, d.n_heads, d.ffn, d.n_layers, d.n_refiner = H, NH, F, n_layers, n_refiner
+    d.adaln_dim, d.time_freq, d.time_mid = adaln, time_freq, time_mid
+    d.patch_dim, d.cap_dim = patch_dim, cap_dim
+    d.eps, d.rope_theta, d.t_scale = 1e-5, 256.0, 1000.0
+    d.axes[:] = [32, 48, 48]
+    d.axes_lens[:] = [4096, 512, 512]
+    for name, obj in dev.items():
+        setattr(d, name, m._h(obj))
+    model = m.Model(ctx, d, cb, mb, keep=keep + [dev, cb, mb])
+    return mo, model
