@@ -121,6 +121,129 @@ def cpu_baseline(hosts, x_host, target_s, threads):
                       f"{dt:.1f} s"}
 
 
+def forward_flops(img, cap):
+    """Algorithmic FLOP of one 34-block forward (GEMM + live LoRA +
+    attention): 2 context-refiner blocks over the caption, 2 noise-refiner
+    blocks over the image, 30 layers over the joint sequence."""
+    R = live_rank()
+    JT = img + cap
+    per_row = 2 * (4 * HID * HID + 3 * HID * FFN)          # q,k,v,o,w1,w3,w2
+    lora_row = 2 * R * (4 * (HID + HID) + 3 * (HID + FFN))
+    rows = 30 * JT + 2 * img + 2 * cap
+    attn = 4 * 30 * 128 * (30 * JT * JT + 2 * img * img + 2 * cap * cap)
+    return rows * (per_row + lora_row) + attn
+
+
+def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2):
+    """A 34-block w4g64 model with random-init weights (quantized on the GPU by
+    the library's pack writer), the config-2 adapter set bound on all seven
+    projections of every block, dense embedders and final layer."""
+    dev = "cuda"
+    keep = []
+
+    def qw(N, K):
+        w = torch.randn((N, K), generator=gen, device=dev) * 0.02
+        codes = torch.empty((N, K // 8), dtype=torch.int32, device=dev)
+        sc = torch.empty((N, K // 64), dtype=torch.int16, device=dev)
+        bi = torch.empty((N, K // 64), dtype=torch.int16, device=dev)
+        torch.cuda.synchronize()
+        ctx.quantize_pack(w, N, K, 4, codes, sc, bi)
+        ctx.synchronize()
+        q = m.QWeight.quantized(ctx, codes, sc, bi, 4, on_device=True)
+        return q
+
+    def lora(q, N, K):
+        for slot, r in enumerate(RANKS):
+            A = (torch.randn((r, K), generator=gen, device=dev) / K ** 0.5
+                 ).to(torch.bfloat16).view(torch.int16)
+            B = (torch.randn((N, r), generator=gen, device=dev) * 0.01
+                 ).to(torch.bfloat16).view(torch.int16)
+            torch.cuda.synchronize()
+            q.bind_lora(slot, A, B, on_device=True)
+
+    def vec(n, base, std):
+        v = (base + std * torch.randn((n,), generator=gen, device=dev))
+        v = v.to(torch.bfloat16).view(torch.int16).contiguous()
+        keep.append(v)
+        return v
+
+    def dense(N, K):
+        w = (torch.randn((N, K), generator=gen, device=dev) / K ** 0.5
+             ).to(torch.bfloat16).view(torch.int16).contiguous()
+        torch.cuda.synchronize()
+        return m.QWeight.dense(ctx, w, on_device=True)
+
+    def block(modulated):
+        parts = {}
+        for name, (N, K) in {"q": (HID, HID), "k": (HID, HID),
+                             "v": (HID, HID), "o": (HID, HID),
+                             "w1": (FFN, HID), "w3": (FFN, HID),
+                             "w2": (HID, FFN)}.items():
+            parts[name] = qw(N, K)
+            lora(parts[name], N, K)
+        if modulated:
+            parts["ada"] = qw(4 * HID, 256)
+            parts["ada_b"] = vec(4 * HID, 0.0, 0.1)
+        for g in ("an1", "an2", "fn1", "fn2"):
+            parts[g] = vec(HID, 1.0, 0.1)
+        parts["nq"] = vec(128, 1.0, 0.1)
+        parts["nk"] = vec(128, 1.0, 0.1)
+        return m.block_desc(**parts)
+
+    cb, mb = [], []
+    for i in range(2 * n_refiner + n_layers):
+        (cb if i < n_refiner else mb).append(block(i >= n_refiner))
+        print(f"bench: forward model block {i + 1}/{2 * n_refiner + n_layers}",
+              file=sys.stderr, flush=True)
+    d = m.ModelDesc()
+    d.hidden, d.n_heads, d.ffn = HID, 30, FFN
+    d.n_layers, d.n_refiner, d.adaln_dim = n_layers, n_refiner, 256
+    d.time_freq, d.time_mid, d.patch_dim, d.cap_dim = 256, 1024, 64, 2560
+    d.eps, d.rope_theta, d.t_scale = 1e-5, 256.0, 1000.0
+    d.axes[:] = [32, 48, 48]
+    d.axes_lens[:] = [1536, 512, 512]
+    tw = {"time_1": dense(1024, 256), "time_1b": vec(1024, 0.0, 0.05),
+          "time_2": dense(256, 1024), "time_2b": vec(256, 0.0, 0.05),
+          "x_in": dense(HID, 64), "x_in_b": vec(HID, 0.0, 0.05),
+          "cap_norm": vec(2560, 1.0, 0.1), "cap_in": dense(HID, 2560),
+          "cap_in_b": vec(HID, 0.0, 0.05), "final_ada": dense(HID, 256),
+          "final_ada_b": vec(HID, 0.0, 0.05), "final_lin": dense(64, HID),
+          "final_lin_b": vec(64, 0.0, 0.05)}
+    for k, v in tw.items():
+        setattr(d, k, m._h(v))
+    return m.Model(ctx, d, cb, mb, keep=keep + [tw, cb, mb])
+
+
+def time_forward(ctx, m, torch, gen, steps, warmup):
+    """34-block forward at 1024^2 (4096 image + 256 caption tokens): ms per
+    forward, host clock around ming_model_forward (synchronous)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    model = build_forward_model(ctx, m, torch, gen)
+    for i, sc in enumerate(SCALES):
+        model.set_lora_scale(i, sc)
+    img, cap, grid = 4096, 256, 64
+    # positions: image (cap + 1, row, col), caption (1 + i, 0, 0)
+    pt = np.concatenate([np.full(img, cap + 1), 1 + np.arange(cap)]).astype(np.int32)
+    ph = np.concatenate([np.arange(img) // grid, np.zeros(cap)]).astype(np.int32)
+    pw = np.concatenate([np.arange(img) % grid, np.zeros(cap)]).astype(np.int32)
+    lat = torch.randn((img, 64), generator=gen, device="cuda").to(
+        torch.bfloat16).view(torch.int16)
+    capt = torch.randn((cap, 2560), generator=gen, device="cuda").to(
+        torch.bfloat16).view(torch.int16)
+    out = torch.empty((img, 64), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        model.forward(lat, capt, 2560, img, cap, cap, pt, ph, pw, 0.5, out)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.forward(lat, capt, 2560, img, cap, cap, pt, ph, pw, 0.5, out)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    flops = forward_flops(img, cap)
+    model.close()
+    return ms, flops
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -129,6 +252,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-forward", action="store_true",
+                    help="skip the 34-block forward at 1024^2")
+    ap.add_argument("--forward-steps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path runs on ONE GPU (asked for {args.gpus}); "
@@ -210,6 +336,7 @@ def main():
                    "parallelism": "1 GPU"},
         "mfma_util": round(value / PEAK_TFLOPS, 4),
         "forward_ms_1024": None,
+        "forward_tflops_1024": None,
         "roofline": {"bound": "mfma", "kernel": qname,
                      "achieved": round(achieved, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
@@ -218,13 +345,18 @@ def main():
                      "flop_per_launch": round(q["flops"] / q["launches"])},
         "kernels": kernels,
     }
+    for w in (w1, w3, w2):
+        w.close()
+    if not args.no_forward:
+        fms, fflops = time_forward(ctx, m, torch, gen, args.forward_steps, 1)
+        out["forward_ms_1024"] = round(fms, 2)
+        out["forward_tflops_1024"] = round(fflops / (fms * 1e-3) / 1e12, 2)
+        out["forward_tflop"] = round(fflops / 1e12, 2)
     if not args.no_cpu:
         import numpy as np
         xh = x.cpu().view(torch.int16).numpy().view(np.uint16)
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(hosts, xh, args.cpu_seconds, threads)
-    for w in (w1, w3, w2):
-        w.close()
     ctx.close()
     print(json.dumps(out))
 
