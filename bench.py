@@ -244,6 +244,23 @@ def time_forward(ctx, m, torch, gen, steps, warmup):
     return ms, flops
 
 
+TRAFFIC_MD = os.path.join(ROOT, "profiles", "qproj_w4_ffn_config2_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed PMC
+    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a known-size copy);
+    None when absent."""
+    try:
+        with open(TRAFFIC_MD) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,6 +272,9 @@ def main():
     ap.add_argument("--no-forward", action="store_true",
                     help="skip the 34-block forward at 1024^2")
     ap.add_argument("--forward-steps", type=int, default=3)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 256 MiB device-to-device three times (the "
+                         "known-size kernel the HBM byte counters are scaled by)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this path runs on ONE GPU (asked for {args.gpus}); "
@@ -263,6 +283,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        n = 256 * 1024 * 1024 // 4
+        src = torch.randint(0, 1 << 30, (n,), dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print("copy calibration: 268435456 bytes read and written per copy")
+        return
     import ming_dit_amd as m
 
     torch.cuda.init()
@@ -340,7 +369,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": qname,
                      "achieved": round(achieved, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(),
                      "avg_launch_us": round(1e3 * q["ms"] / q["launches"], 2),
                      "flop_per_launch": round(q["flops"] / q["launches"])},
         "kernels": kernels,
