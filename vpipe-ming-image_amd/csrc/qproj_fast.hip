@@ -44,24 +44,6 @@ constexpr int BM = 256, BN = 256, BK = 64;
 __device__ __forceinline__ int swz8(int row, int c) { return row * 8 + (c ^ ((row >> 1) & 7)); }
 __device__ __forceinline__ int swz4(int row, int c) { return row * 4 + (c ^ ((row >> 2) & 3)); }
 
-// Workgroup barrier for the DMA ring: this wave's LDS reads are complete
-// (so another wave may DMA over them) and, being an asm with a memory
-// clobber, no LDS access or DMA issue moves across it -- without the
-// vmcnt(0) a __syncthreads() would add, which would drain the ring.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// s_waitcnt immediate for "vmcnt <= v" (gfx9 encoding: vmcnt[3:0] and
-// vmcnt[5:4] at bits 15:14; expcnt and lgkmcnt left at no-wait).
-constexpr unsigned vm_wait(unsigned v) {
-  return (v & 0xFu) | ((v >> 4) << 14) | (0x7u << 4) | (0xFu << 8);
-}
-
-__device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, 0);
-}
-
 // The DMA written as inline asm, for rings whose waits are all
 // explicit: the compiler then sees no LDS store it must order reads
 // against, so it cannot add a drain of its own (its alias tracking of LDS
@@ -556,28 +538,37 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 }
 
 // ---- T = x . A_live^T * coef: the adapters' stacked down-projection --------
-// Block tile 256 rows x 64 ranks, 4 waves x (64 rows x 64 ranks) of
-// v_mfma_f32_32x32x16_bf16, the same three-stage DMA ring, and split-K so
-// even a 320-rank stack over 4352 rows fills the chip: slice s writes f32
-// partials P[s] and xa_reduce sums the slices in a fixed order (no atomics,
-// so the bits do not depend on timing).
+// Block tile 256 rows x 128 stacked ranks; 4 waves in 2 x 2, each 128 rows x
+// 64 ranks (4 x 2 tiles of v_mfma_f32_32x32x16_bf16, D[rank][row], so a lane
+// owns one row and 4 consecutive ranks per register quad). Split-K over
+// kslices so the grid is about one round of the chip; slice s writes f32
+// partials P[s] and lora_xa_reduce_kernel sums the slices in a fixed order
+// (no atomics: the bits do not depend on timing). With one slice the block
+// writes T directly. The stage ring is the projection kernel's: three
+// stages of [x 32 KB | A 16 KB] filled by inline-asm DMA, each wave's DMA
+// group of stage kt+2 issued one per k16 step, the wait + barrier between
+// steps 2 and 3, and step 3 reading the next stage's first fragments.
 __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a,
                                                               float* part,
                                                               int kslices) {
-  constexpr int STG = 256 * 8 + 64 * 8;          // x tile + A tile, 16-B chunks
-  constexpr int PER = 8 + 2;
+  constexpr int STG = 256 * 8 + 128 * 8;         // x tile + A tile, 16-B chunks
+  constexpr int PER = 12;                        // 8 x + 4 A DMAs per wave
   __shared__ uint4 st0[STG], st1[STG], st2[STG];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fk = lane >> 5;
-  const int m0 = blockIdx.x * 256, c0 = blockIdx.y * 64, ks = blockIdx.z;
+  const int wm = wave & 1, wc = wave >> 1;
+  const int m0 = blockIdx.x * 256, c0 = blockIdx.y * 128, ks = blockIdx.z;
   const int KT = a.K / 64;
   const int kt0 = (int)((long long)KT * ks / kslices);
   const int kt1 = (int)((long long)KT * (ks + 1) / kslices);
   const int NT = kt1 - kt0;
   const int mlast = a.M - 1;
+  // a wave whose 64 ranks lie past n_cols (n_cols % 128 == 64) skips its
+  // MFMAs; it still issues and waits like the others
+  const bool live = c0 + 64 * wc < a.n_cols;
 
-  long long xoff[8];
+  uint32_t xoff[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int p = 64 * (8 * wave + i) + lane;
@@ -585,92 +576,131 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
     const int c = (p & 7) ^ ((row >> 1) & 7);
     int m = m0 + row;
     m = m < mlast ? m : mlast;
-    xoff[i] = (long long)m * a.ldx + 8 * c;
+    xoff[i] = (uint32_t)(((long long)m * a.ldx + 8 * c) * 2);
   }
-  // the first live group: a finite row for padding columns (their coef is 0)
+  // A rows: stacked column col -> row 16 * grp[col / 16] + col % 16; padding
+  // groups (and columns past n_cols) read the first live group's rows
+  // (finite; their T columns are exactly 0 or never written)
   const int g_safe = a.grp[0];
-  long long aoff[2];
+  uint32_t aoff[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = 64 * (2 * wave + i) + lane;
+  for (int i = 0; i < 4; ++i) {
+    const int p = 64 * (4 * wave + i) + lane;
     const int r = p >> 3;
     const int c = (p & 7) ^ ((r >> 1) & 7);
     const int col = c0 + r;
-    int g = a.grp[col >> 4];
+    const int g = col < a.n_cols ? a.grp[col >> 4] : -1;
     const int row = g < 0 ? 16 * g_safe : 16 * g + (col & 15);
-    aoff[i] = (long long)row * a.K + 8 * c;
+    aoff[i] = (uint32_t)(((long long)row * a.K + 8 * c) * 2);
   }
-  auto issue = [&](int kt, uint4* S) {
+  auto issue_grp = [&](int g, int kt, const uint4* S) {
+    if (g < 2) {
+      const void* base = a.x + (long long)kt * 64;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      dma16(a.x + xoff[i] + kt * 64, S + 64 * (8 * wave + i));
+      for (int i = 4 * g; i < 4 * g + 4; ++i)
+        dma16_sb(base, xoff[i], lds_addr(S + 64 * (8 * wave + i)));
+    } else {
+      const void* base = a.A + (long long)kt * 64;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      dma16(a.A + aoff[i] + kt * 64, S + 2048 + 64 * (2 * wave + i));
-  };
-  floatx16_t acc[2][2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
-  auto compute = [&](const uint4* S) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int c = 2 * kk + fk;
-      uint4 av[2], xv[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) av[j] = S[2048 + swz8(32 * j + fr, c)];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) xv[i] = S[swz8(64 * wave + 32 * i + fr, c)];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8_t, av[j]), __builtin_bit_cast(bf16x8_t, xv[i]),
-              acc[j][i], 0, 0, 0);
+      for (int i = 0; i < 4; ++i)
+        dma16_sb(base, aoff[i], lds_addr(S + 2048 + 64 * (4 * wave + i)));
     }
   };
-  auto step = [&](int t, uint4* Sc, uint4* Sn) {
-    __builtin_amdgcn_s_waitcnt(vm_wait(PER));
-    ring_barrier();
-    issue(kt0 + (t + 2 < NT ? t + 2 : NT - 1), Sn);
-    if (t < NT) compute(Sc);
-  };
-  issue(kt0, st0);
-  issue(kt0 + (NT > 1 ? 1 : 0), st1);
-  for (int t = 0; t < NT; t += 3) {
-    step(t, st0, st2);
-    step(t + 1, st1, st0);
-    step(t + 2, st2, st1);
-  }
-  __builtin_amdgcn_s_waitcnt(vm_wait(0));
 
+  floatx16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // fragments of one k16 step: x rows 128wm + 32i + fr, A rows 64wc + 32j + fr
+  uint4 xb[4], ab[2];
+  auto read_frags = [&](const uint4* S, int kk, uint4 (&xv)[4], uint4 (&av)[2]) {
+    const int c = 2 * kk + fk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[i] = S[swz8(128 * wm + 32 * i + fr, c)];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) av[j] = S[2048 + swz8(64 * wc + 32 * j + fr, c)];
+  };
+  auto body = [&](int t, const uint4* C, const uint4* Nx, const uint4* Pv) {
+    const int nk = kt0 + (t + 2 < NT ? t + 2 : NT - 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint4 xn[4], an[2];
+      if (kk < 3) {
+        issue_grp(kk, nk, Pv);
+        read_frags(C, kk + 1, xn, an);
+      } else {
+        read_frags(Nx, 0, xn, an);
+      }
+      if (live) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, ab[j]), __builtin_bit_cast(bf16x8_t, xb[i]),
+                acc[i][j], 0, 0, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < 6; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (kk == 2) {
+        ring_wait<PER>();                        // stage t+1 landed, t done
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xb[i] = xn[i];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) ab[j] = an[j];
+    }
+  };
+
+#pragma unroll
+  for (int g = 0; g < 3; ++g) issue_grp(g, kt0, st0);
+#pragma unroll
+  for (int g = 0; g < 3; ++g) issue_grp(g, kt0 + (NT > 1 ? 1 : 0), st1);
+  ring_wait<PER>();
+  read_frags(st0, 0, xb, ab);
+  int t = 0;
+  for (; t + 3 <= NT; t += 3) {
+    body(t, st0, st1, st2);
+    body(t + 1, st1, st2, st0);
+    body(t + 2, st2, st0, st1);
+  }
+  if (NT - t >= 1) body(t, st0, st1, st2);
+  if (NT - t == 2) body(t + 1, st1, st2, st0);
+  ring_wait<0>();                                // no DMA outlives the block
+
+  if (!live) return;
   // D[c][m]: lane owns row m, four consecutive ranks per register quad.
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int m = m0 + 64 * wave + 32 * i + fr;
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + 128 * wm + 32 * i + fr;
     if (m >= a.M) continue;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int c = c0 + 32 * j + 8 * q + 4 * fk;
+        const int c = c0 + 64 * wc + 32 * j + 8 * q + 4 * fk;
         if (kslices == 1) {
           const float f = a.coef[c >> 4];
           uint2 v;
           if (f == 0.0f) {
             v = make_uint2(0, 0);
           } else {
-            v.x = pack_bf16x2(f * acc[j][i][4 * q + 0], f * acc[j][i][4 * q + 1]);
-            v.y = pack_bf16x2(f * acc[j][i][4 * q + 2], f * acc[j][i][4 * q + 3]);
+            v.x = pack_bf16x2(f * acc[i][j][4 * q + 0], f * acc[i][j][4 * q + 1]);
+            v.y = pack_bf16x2(f * acc[i][j][4 * q + 2], f * acc[i][j][4 * q + 3]);
           }
           *reinterpret_cast<uint2*>(a.t + (long long)m * a.ldt + c) = v;
         } else {
-          float4 v = make_float4(acc[j][i][4 * q + 0], acc[j][i][4 * q + 1],
-                                 acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
+          float4 v = make_float4(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1],
+                                 acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
           *reinterpret_cast<float4*>(
               part + ((long long)ks * a.M + m) * a.n_cols + c) = v;
         }
@@ -795,10 +825,10 @@ hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s) {
 }
 
 int lora_xa_fast_slices(int M, int n_cols, int K) {
-  const int tiles = ((M + 255) / 256) * (n_cols / 64);
+  const int tiles = ((M + 255) / 256) * ((n_cols + 127) / 128);
   const int KT = K / 64;
-  int ks = (512 + tiles - 1) / tiles;          // aim at ~2 blocks per CU
-  const int kmax = KT / 6 > 1 ? KT / 6 : 1;     // keep >= 6 K steps per slice
+  int ks = 256 / (tiles > 0 ? tiles : 1);       // about one round of the chip
+  const int kmax = KT / 8 > 1 ? KT / 8 : 1;      // keep >= 8 K steps per slice
   if (ks > kmax) ks = kmax;
   return ks < 1 ? 1 : ks;
 }
@@ -806,7 +836,7 @@ int lora_xa_fast_slices(int M, int n_cols, int K) {
 hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s) {
   if (a.M <= 0 || a.n_cols <= 0) return hipSuccess;
-  dim3 grid((a.M + 255) / 256, a.n_cols / 64, kslices);
+  dim3 grid((a.M + 255) / 256, (a.n_cols + 127) / 128, kslices);
   hipLaunchKernelGGL(lora_xa_fast_kernel, grid, dim3(256), 0, s, a, part, kslices);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || kslices == 1) return e;

@@ -157,6 +157,7 @@ struct ming_qweight {
   uint16_t* A_all = nullptr;
   std::vector<uint16_t*> B_seg;
   std::vector<int> a_row0;   // [seg*8 + slot] row in A_all
+  int a_rows = 0;            // rows of A_all
   std::vector<int> b_col0;   // [seg*8 + slot] column in B_seg[seg]
   std::vector<int> b_ld;     // per segment: R16 of the segment
 };
@@ -196,6 +197,7 @@ int build_stacks(ming_qweight* q) {
     }
     q->b_ld[si] = col;
   }
+  q->a_rows = rows_all;
   if (rows_all == 0) {
     q->stacks_dirty = false;
     return MING_OK;
@@ -769,7 +771,11 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
         if (b.rank > 0 && scales && scales[sl] != 0.0f)
           xa_flops += 2.0 * M * b.rank * (double)q->K;
       }
-    const bool xa_fast = c->route != MING_ROUTE_GENERAL && ldx % 8 == 0;
+    // the fast x.A addresses x and the A stack as 64-bit bases plus 32-bit
+    // byte offsets
+    const bool xa_fast = c->route != MING_ROUTE_GENERAL && ldx % 8 == 0 &&
+                         (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) &&
+                         (uint64_t)q->a_rows * (uint64_t)q->K * 2 <= (1ull << 32);
     int ks = 1;
     if (xa_fast) {
       ks = ming::lora_xa_fast_slices(M, t_cols, q->K);
