@@ -164,6 +164,20 @@ int ming_lin(ming_ctx* ctx, const ming_qweight* qw, const uint16_t* x,
              int64_t ldx, uint16_t* y, int64_t ldy, int M,
              const float* scales);
 
+/* out = bf16(silu(g) * bf16(lin(x, w))): the w3 projection with the SwiGLU
+ * of gpu_ff (ming-dit.cc:2151-2158; ming_ops.metal:97-112) fused into its
+ * epilogue. Same bits as ming_lin then ming_swiglu. g may be out (in place).
+ * g and out: strides multiples of 8, 16-byte aligned. */
+int ming_lin_swiglu(ming_ctx* ctx, const ming_qweight* w, const uint16_t* x,
+                    int64_t ldx, const uint16_t* g, int64_t ldg, uint16_t* out,
+                    int64_t ldo, int M, const float* scales);
+/* gpu_ff (ming-dit.cc:2151-2162): h = lin(x, w1); h = swiglu(h, lin(x, w3));
+ * y = lin(h, w2), with the live LoRA of each projection. h is the caller's
+ * [M][ffn] plane (ldh >= ffn, a multiple of 8, 16-byte aligned). Same bits
+ * as the four separate calls; x is converted for the fast route once. */
+int ming_ffn(ming_ctx* ctx, const ming_qweight* w1, const ming_qweight* w3,
+             const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
+             int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh);
 /* ---- norms and rotary ----------------------------------------------------------
  * rms (ming-dit.cc:1780-1787): y = bf16(x * rsqrt(mean(x^2)+eps) * w) per
  * row of D (D % 8 == 0, D <= 8192); in place when x == y. */

@@ -272,3 +272,68 @@ def test_routes_agree(ctx, orc, bits, route):
     yg = _run(ctx, qw, x, M, sc)
     ctx.set_route("auto")
     assert orc.rel_l2(orc.bf16_to_f32(yf), orc.bf16_to_f32(yg)) < 5e-4
+
+
+def _ffn_weights(ctx, seed, H, F, bits=4, slots=CFG2_RANKS):
+    ws = []
+    for i, (N, K) in enumerate(((F, H), (F, H), (H, F))):
+        pack, _ = make_weight(seed + i, N, K, bits)
+        qw = _qw(ctx, pack, bits)
+        for s, r in enumerate(slots):
+            A, B = make_lora(seed + 10 * i + 2 * s + 100, N, K, r)
+            qw.bind_lora(s, A, B)
+        ws.append(qw)
+    return ws
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_lin_swiglu_equals_lin_then_swiglu(ctx, orc, inplace):
+    """The SwiGLU fused into the projection epilogue gives the bits of
+    ming_lin followed by ming_swiglu (gpu_ff, ming-dit.cc:2151-2158)."""
+    M, H, F = 300, 384, 640
+    w1, w3, _ = _ffn_weights(ctx, 610, H, F)
+    x = to_dev(bf16(randn(611, (M, H))))
+    g = to_dev(bf16(randn(612, (M, F))))
+    u = _run(ctx, w3, x, M, CFG2_SCALES)
+    ref = empty_bf16(M, F)
+    ud = to_dev(u)
+    sync()
+    ctx.swiglu(g, ud, ref, M, F)
+    sync()
+    out = g.clone() if inplace else empty_bf16(M, F)
+    sync()
+    ctx.lin_swiglu(w3, x, out if inplace else g, out, M, CFG2_SCALES)
+    sync()
+    assert np.array_equal(from_dev(out), from_dev(ref))
+
+
+def test_ffn_equals_the_four_calls(ctx, orc):
+    """ming_ffn == lin(w1), lin(w3), swiglu, lin(w2) bit for bit, with the
+    config-2 adapter set live on all three projections."""
+    M, H, F = 260, 384, 640
+    w1, w3, w2 = _ffn_weights(ctx, 620, H, F)
+    x = to_dev(bf16(randn(621, (M, H))))
+    g = to_dev(_run(ctx, w1, x, M, CFG2_SCALES))
+    u = to_dev(_run(ctx, w3, x, M, CFG2_SCALES))
+    a = empty_bf16(M, F)
+    sync()
+    ctx.swiglu(g, u, a, M, F)
+    sync()
+    ref = _run(ctx, w2, a, M, CFG2_SCALES)
+    y = empty_bf16(M, H)
+    e0 = ctx.engagement()
+    ctx.ffn(w1, w3, w2, x, y, M, CFG2_SCALES)
+    sync()
+    e1 = ctx.engagement()
+    assert e1["gemm_q4"] - e0["gemm_q4"] == 3
+    assert e1["lora_proj"] - e0["lora_proj"] == 3
+    assert np.array_equal(from_dev(y), ref)
+
+
+def test_ffn_rejects_mismatched_shapes(ctx):
+    M, H, F = 64, 256, 512
+    w1, w3, w2 = _ffn_weights(ctx, 630, H, F)
+    x = to_dev(bf16(randn(631, (M, H))))
+    y = empty_bf16(M, H)
+    with pytest.raises(m.MingError):
+        ctx.ffn(w1, w2, w2, x, y, M)

@@ -44,6 +44,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// silu(g) = g / (1 + exp(-g)) in f32: the SwiGLU gate (ming_ops.metal:97-112).
+// One definition for the standalone SwiGLU and the projection epilogue that
+// fuses it, so the two give the same bits.
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
 // Two bf16 (one u32) -> two fp16 (one u32). Exact for every value inside
 // fp16's range, so the rounding mode of the packed conversion is moot.
 __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u) {

@@ -19,8 +19,6 @@
 namespace ming {
 namespace {
 
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
-
 __global__ void swiglu_kernel(const uint16_t* g, long long ldg,
                               const uint16_t* u, long long ldu, uint16_t* out,
                               long long ldo, int rows, int n) {

@@ -47,6 +47,10 @@ struct QprojArgs {
   const uint16_t* t;
   int ldt;
   int nseg;
+  // optional SwiGLU gate: when g != nullptr the output is
+  // y = bf16(silu(g) * bf16(x . W^T + LoRA)) (g bf16 [M][ldg], may equal y)
+  const uint16_t* g;
+  long long ldg;
   QprojSeg seg[kMaxSeg];
   int16_t grp[kMaxGroups];
 };

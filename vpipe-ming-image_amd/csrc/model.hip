@@ -36,16 +36,16 @@ using ming::rt_ok;
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct BlockWs {
-  uint16_t *nrm, *qkv, *ob, *ffg, *ffu, *mods, *nw1, *nw3;
+  uint16_t *nrm, *qkv, *ob, *ffg, *mods, *nw1, *nw3;
 };
 
 size_t block_ws_layout(const ming_block_dims& d, int rows, char* base, BlockWs* w) {
   const size_t H = (size_t)d.hidden, F = (size_t)d.ffn, R = (size_t)rows;
-  const size_t sz[8] = {R * H * 2, R * 3 * H * 2, R * H * 2, R * F * 2,
-                        R * F * 2, 4 * H * 2,     H * 2,     H * 2};
-  uint16_t** dst[8] = {&w->nrm, &w->qkv, &w->ob, &w->ffg, &w->ffu, &w->mods, &w->nw1, &w->nw3};
+  const size_t sz[7] = {R * H * 2, R * 3 * H * 2, R * H * 2, R * F * 2,
+                        4 * H * 2, H * 2,         H * 2};
+  uint16_t** dst[7] = {&w->nrm, &w->qkv, &w->ob, &w->ffg, &w->mods, &w->nw1, &w->nw3};
   size_t off = 0;
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 7; ++i) {
     if (base) *dst[i] = reinterpret_cast<uint16_t*>(base + off);
     off += align256(sz[i]);
   }
@@ -124,12 +124,9 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
   } else {
     RC(ming_residual_add(c, x, H, w.ob, H, rows, H));
   }
-  // ---- feed-forward half (gpu_ff, 2151-2162) ----
+  // ---- feed-forward half (gpu_ff, 2151-2162; SwiGLU fused into w3) ----
   RC(ming_rmsnorm(c, x, H, g3, w.nrm, H, rows, H, eps));
-  RC(ming_lin(c, b->w1, w.nrm, H, w.ffg, F, rows, scales));
-  RC(ming_lin(c, b->w3, w.nrm, H, w.ffu, F, rows, scales));
-  RC(ming_swiglu(c, w.ffg, F, w.ffu, F, w.ffg, F, rows, F));
-  RC(ming_lin(c, b->w2, w.ffg, F, w.ob, H, rows, scales));
+  RC(ming_ffn(c, b->w1, b->w3, b->w2, w.nrm, H, w.ob, H, rows, scales, w.ffg, F));
   RC(ming_rmsnorm(c, w.ob, H, b->fn2, w.ob, H, rows, H, eps));
   if (modulated) {
     RC(ming_gated_residual(c, x, H, w.mods + 3 * H, w.ob, H, rows, H));

@@ -522,9 +522,19 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int ml = 8 * r + (lane >> 3);
-      const uint4 v = E[ml * 8 + (cl ^ ((ml >> 1) & 7))];
+      uint4 v = E[ml * 8 + (cl ^ ((ml >> 1) & 7))];
       const int m = m0 + 128 * h + ml;
       if (m < a.M && n < a.N) {
+        if (a.g) {
+          // fused SwiGLU: the bf16 projection output is the "up" operand
+          const uint4 gv = *reinterpret_cast<const uint4*>(a.g + (long long)m * a.ldg + n);
+          const uint32_t* gp = &gv.x;
+          uint32_t* vp = &v.x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            vp[e] = pack_bf16x2(silu_f(bf16_lo(gp[e])) * bf16_lo(vp[e]),
+                                silu_f(bf16_hi(gp[e])) * bf16_hi(vp[e]));
+        }
         uint16_t* yp = a.y + (long long)m * a.ldy + n;
         if (st16) {
           *reinterpret_cast<uint4*>(yp) = v;

@@ -67,6 +67,8 @@ struct ming_ctx {
   size_t xh_bytes = 0;
   void* vt = nullptr;          // V^T [heads][128][keys] for attention
   size_t vt_bytes = 0;
+  void* up = nullptr;          // general route + SwiGLU: the projection before the gate
+  size_t up_bytes = 0;
   void* part = nullptr;        // split-K partials of the stacked x.A GEMM
   size_t part_bytes = 0;
   int route = MING_ROUTE_AUTO;
@@ -281,6 +283,18 @@ int ensure_vt(ming_ctx* c, size_t bytes) {
   return MING_OK;
 }
 
+int ensure_up(ming_ctx* c, size_t bytes) {
+  if (bytes <= c->up_bytes) return MING_OK;
+  MING_HIP(hipStreamSynchronize(c->stream), "scratch grow sync");
+  if (c->up) (void)hipFree(c->up);
+  c->up = nullptr;
+  c->up_bytes = 0;
+  if (hipMalloc(&c->up, bytes) != hipSuccess)
+    return fail(MING_ERR_ALLOC, "SwiGLU scratch allocation failed");
+  c->up_bytes = bytes;
+  return MING_OK;
+}
+
 // Copy `bytes` from host or device into a fresh device buffer.
 int upload(ming_ctx* c, void** dst, const void* src, size_t bytes,
            int src_on_device) {
@@ -372,6 +386,7 @@ int ming_ctx_destroy(ming_ctx* c) {
   if (c->scratch) (void)hipFree(c->scratch);
   if (c->xh) (void)hipFree(c->xh);
   if (c->vt) (void)hipFree(c->vt);
+  if (c->up) (void)hipFree(c->up);
   if (c->part) (void)hipFree(c->part);
   for (auto& rec : c->recs) {
     (void)hipEventDestroy(rec.a);
@@ -682,9 +697,15 @@ int ming_qweight_lora_rank(const ming_qweight* q, int segment, int slot) {
   return q->segs[segment].slot[slot].rank;
 }
 
-int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
-             int64_t ldx, uint16_t* y, int64_t ldy, int M,
-             const float* scales) {
+// The projection with its options: `gate` fuses SwiGLU into the output
+// (y = bf16(silu(gate) * bf16(lin(x)))), `xh_ready` says the context's fp16
+// copy of x already holds this x (the fast route then skips its conversion),
+// and *took_fast reports whether the fast route ran.
+static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
+                    int64_t ldx, uint16_t* y, int64_t ldy, int M,
+                    const float* scales, const uint16_t* gate, int64_t ldg,
+                    bool xh_ready, bool* took_fast) {
+  if (took_fast) *took_fast = false;
   if (!c || !qc || !x || !y) return fail(MING_ERR_ARG, "ming_lin: null argument");
   if (qc->ctx != c) return fail(MING_ERR_ARG, "ming_lin: weight of another context");
   ming_qweight* q = const_cast<ming_qweight*>(qc);
@@ -694,6 +715,11 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
                 "ming_lin: need ldx >= K, ldx % 8 == 0, ldy >= N, ldy % 4 == 0");
   if (!aligned(x, 16) || !aligned(y, 8))
     return fail(MING_ERR_ARG, "ming_lin: x must be 16-byte and y 8-byte aligned");
+  if (gate && (ldg < q->N || ldg % 8 != 0 || !aligned(gate, 16) || ldy % 8 != 0 ||
+               !aligned(y, 16)))
+    return fail(MING_ERR_SHAPE,
+                "ming_lin_swiglu: gate and output need strides % 8 == 0 and 16-byte "
+                "alignment (ldg >= N)");
   if (M == 0) return ok();
   DeviceGuard g(c->device);
 
@@ -805,17 +831,28 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
   const bool fast = q->bits != 16 && q->fast && c->route != MING_ROUTE_GENERAL && fits32;
   qa.x = x; qa.ldx = ldx; qa.codes = q->codes_t; qa.sb = q->sb; qa.w16 = q->w16;
   qa.y = y; qa.ldy = ldy; qa.M = M; qa.N = q->N; qa.K = q->K;
+  if (gate && !fast) {
+    // the general route writes the projection first: into a plane of its
+    // own, since y may be the gate itself
+    int rc = ensure_up(c, (size_t)M * q->N * 2);
+    if (rc != MING_OK) return rc;
+    qa.y = (uint16_t*)c->up; qa.ldy = q->N;
+  }
   qa.t = T; qa.ldt = t_cols > 0 ? t_cols : 0; qa.nseg = nseg;
+  qa.g = nullptr; qa.ldg = 0;
   if (fast) {
     // The fast route reads x as fp16 carrying the same (bf16) values.
-    int rc = ensure_xh(c, (size_t)M * q->K * 2);
-    if (rc != MING_OK) return rc;
-    uint16_t* xh = (uint16_t*)c->xh;
-    MING_HIP(profiled(c, kBCvt, 0.0, 4.0 * M * q->K,
-                      [&] { return ming::launch_bf16_to_f16(x, ldx, xh, q->K, M,
-                                                            q->K, c->stream); }),
-             "bf16->fp16 launch");
-    qa.x = xh; qa.ldx = q->K; qa.codes = q->codes_f; qa.sb = q->sbf;
+    if (!xh_ready) {
+      int rc = ensure_xh(c, (size_t)M * q->K * 2);
+      if (rc != MING_OK) return rc;
+      uint16_t* xh = (uint16_t*)c->xh;
+      MING_HIP(profiled(c, kBCvt, 0.0, 4.0 * M * q->K,
+                        [&] { return ming::launch_bf16_to_f16(x, ldx, xh, q->K, M,
+                                                              q->K, c->stream); }),
+               "bf16->fp16 launch");
+    }
+    qa.x = (const uint16_t*)c->xh; qa.ldx = q->K; qa.codes = q->codes_f; qa.sb = q->sbf;
+    qa.g = gate; qa.ldg = ldg;       // the fast epilogue fuses SwiGLU
   }
   const double base_flops = 2.0 * M * (double)q->N * q->K;
   double tail_flops = 0.0;
@@ -837,6 +874,16 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
                                   : ming::launch_qproj(q->bits, qa, c->stream);
                     }),
            "qproj launch");
+  if (gate && !fast) {
+    // the general route writes the projection; SwiGLU follows in place
+    MING_HIP(profiled(c, kBSwiglu, 0.0, 6.0 * M * q->N,
+                      [&] { return ming::launch_swiglu(gate, ldg, (const uint16_t*)c->up,
+                                                       q->N, y, ldy, M, q->N,
+                                                       c->stream); }),
+             "swiglu launch");
+  }
+  if (gate) c->eng.elementwise += 1;
+  if (took_fast) *took_fast = fast;
   if (fast) c->eng.gemm_fast += 1;
   if (q->bits == 4) c->eng.gemm_q4 += 1;
   else if (q->bits == 8) c->eng.gemm_q8 += 1;
@@ -844,6 +891,38 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
   c->eng.lora_proj += live_segs;
   c->eng.gemm_flops += 2ull * (uint64_t)M * (uint64_t)q->N * (uint64_t)q->K + lora_flops;
   return ok();
+}
+
+int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
+             int64_t ldx, uint16_t* y, int64_t ldy, int M,
+             const float* scales) {
+  return lin_impl(c, qc, x, ldx, y, ldy, M, scales, nullptr, 0, false, nullptr);
+}
+
+int ming_lin_swiglu(ming_ctx* c, const ming_qweight* w, const uint16_t* x,
+                    int64_t ldx, const uint16_t* g, int64_t ldg, uint16_t* out,
+                    int64_t ldo, int M, const float* scales) {
+  if (!g) return fail(MING_ERR_ARG, "ming_lin_swiglu: null gate");
+  return lin_impl(c, w, x, ldx, out, ldo, M, scales, g, ldg, false, nullptr);
+}
+
+int ming_ffn(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
+             const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
+             int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh) {
+  if (!c || !w1 || !w3 || !w2 || !x || !y || !h)
+    return fail(MING_ERR_ARG, "ming_ffn: null argument");
+  const int F = w1->N, H = w1->K;
+  if (w3->N != F || w3->K != H || w2->N != H || w2->K != F)
+    return fail(MING_ERR_SHAPE, "ming_ffn: need w1, w3 [ffn][H] and w2 [H][ffn]");
+  if (ldh < F || ldh % 8 != 0 || !aligned(h, 16))
+    return fail(MING_ERR_SHAPE, "ming_ffn: h needs ldh >= ffn, ldh % 8 == 0, 16-byte alignment");
+  bool fast1 = false;
+  int rc = lin_impl(c, w1, x, ldx, h, ldh, M, scales, nullptr, 0, false, &fast1);
+  if (rc != MING_OK) return rc;
+  // w3 reads the same x: the fp16 copy w1's fast route made serves it too
+  rc = lin_impl(c, w3, x, ldx, h, ldh, M, scales, h, ldh, fast1, nullptr);
+  if (rc != MING_OK) return rc;
+  return lin_impl(c, w2, h, ldh, y, ldy, M, scales, nullptr, 0, false, nullptr);
 }
 
 int ming_rmsnorm(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* w,

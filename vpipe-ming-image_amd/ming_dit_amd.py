@@ -127,6 +127,10 @@ def lib():
         "ming_silu": ([vp, vp, vp, i32], i32),
         "ming_ln_modulate": ([vp, vp, i64, vp, vp, i64, i32, i32, f32], i32),
         "ming_quantize_pack": ([vp, vp, i32, i32, i32, i32, vp, vp, vp], i32),
+        "ming_lin_swiglu": ([vp, vp, vp, i64, vp, i64, vp, i64, i32,
+                             C.POINTER(f32)], i32),
+        "ming_ffn": ([vp, vp, vp, vp, vp, i64, vp, i64, i32, C.POINTER(f32),
+                      vp, i64], i32),
         "ming_block_workspace_bytes": ([C.POINTER(BlockDims), i32], C.c_size_t),
         "ming_block_forward": ([vp, C.POINTER(BlockDesc), C.POINTER(BlockDims),
                                 vp, i32, vp, vp, vp, C.POINTER(f32), vp,
@@ -235,6 +239,25 @@ class Ctx:
         ldy = qw.N if ldy is None else ldy
         _check(lib().ming_lin(self.h, qw.h, _ptr(x), ldx, _ptr(y), ldy, M,
                               _scales(scales)))
+
+    def lin_swiglu(self, w: "QWeight", x, g, out, M: int, scales=None,
+                   ldx=None, ldg=None, ldo=None):
+        """out = bf16(silu(g) * lin(x, w)); g may be out."""
+        _check(lib().ming_lin_swiglu(self.h, w.h, _ptr(x), ldx or w.K, _ptr(g),
+                                     ldg or w.N, _ptr(out), ldo or w.N, M,
+                                     _scales(scales)))
+
+    def ffn(self, w1: "QWeight", w3: "QWeight", w2: "QWeight", x, y, M: int,
+            scales=None, h=None, ldx=None, ldy=None, ldh=None):
+        """gpu_ff: y = lin(swiglu(lin(x, w1), lin(x, w3)), w2); h is the
+        [M][ffn] intermediate plane (allocated here when None)."""
+        if h is None:
+            import torch
+            h = torch.empty((M, w1.N), dtype=torch.int16, device="cuda")
+        _check(lib().ming_ffn(self.h, w1.h, w3.h, w2.h, _ptr(x), ldx or w1.K,
+                              _ptr(y), ldy or w2.N, M, _scales(scales), _ptr(h),
+                              ldh or w1.N))
+        return h
 
     def rmsnorm(self, x, w, y, rows: int, D: int, eps: float = 1e-5,
                 ldx=None, ldy=None):
