@@ -46,8 +46,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
 
 // silu(g) = g / (1 + exp(-g)) in f32: the SwiGLU gate (ming_ops.metal:97-112).
 // One definition for the standalone SwiGLU and the projection epilogue that
-// fuses it, so the two give the same bits.
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+// fuses it, so the two give the same bits. The hardware base-2 exponential
+// and reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each) replace expf's
+// range reduction and the IEEE divide: two transcendental ops per element
+// instead of ~30 VALU ops, which matters in the projection epilogue where one
+// wave per SIMD leaves nothing to hide them behind. Limits: g -> -inf gives
+// e = inf, rcp = 0, silu = -0; g -> +inf gives e = 0, silu = g.
+__device__ __forceinline__ float silu_f(float g) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 // Two bf16 (one u32) -> two fp16 (one u32). Exact for every value inside
 // fp16's range, so the rounding mode of the packed conversion is moot.

@@ -22,12 +22,13 @@ namespace {
 __global__ void swiglu_kernel(const uint16_t* g, long long ldg,
                               const uint16_t* u, long long ldu, uint16_t* out,
                               long long ldo, int rows, int n) {
+  // blockIdx.x walks the columns, blockIdx.y the rows (grid-stride in both),
+  // so no 64-bit division per vector.
   const int n8 = n >> 3;
-  const long long total = (long long)rows * n8;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-       i += (long long)gridDim.x * blockDim.x) {
-    const long long r = i / n8;
-    const int c = (int)(i % n8) * 8;
+  for (int r = blockIdx.y; r < rows; r += gridDim.y)
+  for (int c8 = blockIdx.x * blockDim.x + threadIdx.x; c8 < n8;
+       c8 += gridDim.x * blockDim.x) {
+    const int c = c8 * 8;
     const uint4 gv = *reinterpret_cast<const uint4*>(g + r * ldg + c);
     const uint4 uv = *reinterpret_cast<const uint4*>(u + r * ldu + c);
     const uint32_t* gp = &gv.x;
@@ -204,8 +205,10 @@ unsigned grid_for(long long work) {
 hipError_t launch_swiglu(const uint16_t* g, long long ldg, const uint16_t* u,
                          long long ldu, uint16_t* out, long long ldo, int rows,
                          int n, hipStream_t s) {
-  hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for((long long)rows * n / 8)),
-                     dim3(256), 0, s, g, ldg, u, ldu, out, ldo, rows, n);
+  const unsigned gx = (unsigned)(n / 8 + 255) / 256;
+  const unsigned gy = (unsigned)(rows < 1 ? 1 : rows > 65535 ? 65535 : rows);
+  hipLaunchKernelGGL(swiglu_kernel, dim3(gx < 1 ? 1 : gx, gy), dim3(256), 0, s,
+                     g, ldg, u, ldu, out, ldo, rows, n);
   return hipGetLastError();
 }
 

@@ -499,8 +499,22 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
   // of one wave complete in order, so no barrier is needed inside.
   uint4* const E = (wave < 2 ? st0 : st1) + 1024 * (wave & 1);
   const bool st16 = (a.ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+  const int cl = lane & 7;
+  const int n = n0 + 64 * wave + 8 * cl;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
+    // Fused SwiGLU: this half's gate rows are loaded first, so their memory
+    // latency overlaps the conversion below instead of stalling each store.
+    uint4 gv[16];
+    if (a.g) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        int m = m0 + 128 * h + 8 * r + (lane >> 3);
+        m = m < a.M ? m : a.M - 1;
+        const int nn = n < a.N ? n : a.N - 8;
+        gv[r] = *reinterpret_cast<const uint4*>(a.g + (long long)m * a.ldg + nn);
+      }
+    }
     uint2* const E2 = reinterpret_cast<uint2*>(E);
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
@@ -517,8 +531,6 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
           E2[ml * 16 + 2 * (c ^ ((ml >> 1) & 7)) + fk] = v;
         }
     }
-    const int cl = lane & 7;
-    const int n = n0 + 64 * wave + 8 * cl;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int ml = 8 * r + (lane >> 3);
@@ -526,9 +538,8 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
       const int m = m0 + 128 * h + ml;
       if (m < a.M && n < a.N) {
         if (a.g) {
-          // fused SwiGLU: the bf16 projection output is the "up" operand
-          const uint4 gv = *reinterpret_cast<const uint4*>(a.g + (long long)m * a.ldg + n);
-          const uint32_t* gp = &gv.x;
+          // the bf16 projection output is the "up" operand
+          const uint32_t* gp = &gv[r].x;
           uint32_t* vp = &v.x;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
