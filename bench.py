@@ -221,6 +221,9 @@ def time_forward(ctx, m, torch, gen, steps, warmup):
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     model = build_forward_model(ctx, m, torch, gen)
+    # every forward runs all 34 blocks: the caption cache (which would serve
+    # the context refiner from the previous forward) is off
+    model.set_caption_cache(False)
     for i, sc in enumerate(SCALES):
         model.set_lora_scale(i, sc)
     img, cap, grid = 4096, 256, 64

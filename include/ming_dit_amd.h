@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MING_ABI_VERSION 1
+#define MING_ABI_VERSION 2
 
 /* Runtime-LoRA slots: lora::Stack::kMax (ming-dit.h:117) and the eight
  * `lora`..`lora8` keys (ming-model-config-stage.h:37-56). */
@@ -63,6 +63,7 @@ typedef struct ming_engagement {
   int64_t elementwise;
   uint64_t gemm_flops;  /* 2*M*N*K + sum_live 2*M*r*(K+N) per projection */
   int64_t gemm_fast;    /* of the quantized projections, those on the fast route */
+  int64_t cap_cache_hits; /* forwards whose caption path came from the caption cache */
 } ming_engagement;
 
 /* Kernel routes for quantized projections. AUTO takes the fast route
@@ -88,6 +89,15 @@ typedef struct ming_profile_bucket {
 /* Last error of the CALLING thread; "" when the last call succeeded. */
 const char* ming_last_error(void);
 int ming_abi_version(void);
+
+/* The session log (the reference's SessionContextIntf warn / log_normal):
+ * binding reports and refusals that are not errors go here. level 1 warn,
+ * 2 info. NULL restores the default, which drops the messages. The sink is
+ * process-wide and called on the thread that makes the call being reported. */
+#define MING_LOG_WARN 1
+#define MING_LOG_INFO 2
+typedef void (*ming_log_fn)(void* user, int level, const char* message);
+void ming_set_log_sink(ming_log_fn fn, void* user);
 
 /* ---- context --------------------------------------------------------------
  * Binds a device and a stream (NULL: the context creates and owns one).
@@ -350,6 +360,105 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
                        int64_t cap_stride, int img_tokens, int cap_len, int query_rows,
                        const int32_t* pos_t, const int32_t* pos_h, const int32_t* pos_w,
                        float sigma, uint16_t* out);
+
+/* ---- lifecycle (set_stream_stop, set_block_progress, set_caption_cache;
+ * ming-dit.h:191-193, 221-223) ------------------------------------------------
+ * stop: polled on the calling thread before every block; non-zero stops the
+ * forward, which then returns MING_STOPPED with an empty error and leaves
+ * `out` unwritten. While a stop callback is set the forward waits for the
+ * GPU every 4 modulated blocks, so a stop is seen within a few blocks
+ * (kStopDrainBlocks, ming-dit.cc:2530-2540). NULL clears it. */
+typedef int (*ming_stop_fn)(void* user);
+int ming_model_set_stream_stop(ming_model* m, ming_stop_fn fn, void* user);
+/* progress(user, done, total): once per block, in order, done = 0 .. total-1
+ * (blocks finished BEFORE that block; total = 2 * n_refiner + n_layers). A
+ * report is made only after those blocks have finished on the GPU, on the
+ * calling thread, before ming_model_forward returns. NULL clears it. */
+typedef void (*ming_progress_fn)(void* user, int done, int total);
+int ming_model_set_block_progress(ming_model* m, ming_progress_fn fn, void* user);
+/* The per-caption cache (on by default): the context-refined caption rows of
+ * the last two captions, keyed on the caption's exact bytes, length, query
+ * rows and stride (ming-dit.cc:1543-1577). A hit skips cap_embedder and the
+ * context refiner. A strength change on a slot bound in the context refiner,
+ * and any rebinding, drops it. Off frees it. */
+int ming_model_set_caption_cache(ming_model* m, int on);
+
+/* ---- checkpoints and packs (load_qw_ + pack detection, ming-dit.cc:802-831,
+ * 1115-1135; read_dit_config, ming-config.cc:90-137) -------------------------
+ * A transformer directory: config.json (a DiffusionTransformer with the Ming
+ * checkpoint contract) and one or more .safetensors files. A pack carries
+ * `<name>.scales` beside its codes; quantization is read off the tensors,
+ * not the config: group = dim / to_q.scales.cols, bits = codes.cols * 32 / K. */
+typedef struct ming_dit_config {
+  int dim, n_layers, n_refiner_layers, n_heads, n_kv_heads, in_channels;
+  int patch, f_patch, cap_feat_dim, qk_norm;
+  float norm_eps, rope_theta, t_scale;
+  int axes_dims[3], axes_lens[3];
+  int zero_masked;          /* alignment_padding_mode: 1 "zero_masked", 0 "learned" */
+  int multi_frame_output;
+  /* derived as the reference derives them (cfg_from_, ming-dit.cc:296-366) */
+  int ffn_inner;            /* int(dim / 3 * 8) */
+  int adaln_dim;            /* min(dim, 256) */
+  int time_mid, time_freq;  /* 1024, 256 */
+  int patch_dim;            /* f_patch * patch^2 * in_channels */
+} ming_dit_config;
+
+typedef struct ming_pack ming_pack;
+/* Reads config.json and maps every .safetensors file (nothing is copied).
+ * Refuses a directory that is not a Ming-Image transformer. */
+int ming_pack_open(const char* transformer_dir, ming_pack** out);
+int ming_pack_close(ming_pack* p);
+int ming_pack_config(const ming_pack* p, ming_dit_config* out);
+/* 4 or 8 for a pack, 0 for a dense checkpoint; group 64 for a pack. */
+int ming_pack_quant_bits(const ming_pack* p);
+int ming_pack_group(const ming_pack* p);
+int ming_pack_tensor_count(const ming_pack* p);
+/* Name of tensor i (file order), NULL past the end. */
+const char* ming_pack_tensor_name(const ming_pack* p, int i);
+/* dtype (e.g. "BF16", "U32"; 8 bytes with the NUL), shape (up to 8 dims). */
+int ming_pack_tensor_info(const ming_pack* p, const char* name, char* dtype8,
+                          int64_t* shape8, int* ndim);
+/* Projections held quantized (codes + scales + biases): 270 in the 34-block model. */
+int ming_pack_quantized_count(const ming_pack* p);
+/* model-quantize for this family (ming-quant-family.cc:31-59): every 2-D float
+ * tensor of the block stacks whose leaf is not a norm, at `bits` (4 affine or 8
+ * symmetric, group 64, the recipe of ming_quantize_pack) as codes U32 + scales
+ * + biases BF16; every other tensor BF16; config.json kept key for key with
+ * "quantization": {"bits", "group_size": 64} and "_vpipe_component":
+ * "ming-image-dit" added. Host only (no GPU); `threads` <= 0 uses all cores. */
+int ming_pack_write(const char* src_dir, const char* dst_dir, int bits, int threads);
+
+/* ---- runtime LoRA from adapter files (bind_loras_, ming-dit.cc:2918-3005) -----
+ * One .safetensors per slot, POSITIONAL: spec i binds slot i, an empty or NULL
+ * path leaves its slot unbound, specs past slot 8 are reported and ignored.
+ * Module names are the model's own (`layers.<i>.attention.to_q`, ...,
+ * `feed_forward.w2` over context_refiner / noise_refiner / layers), read under
+ * the `transformer.`, `diffusion_model.` and `base_model.model.` prefixes,
+ * with `.lora_A` / `.lora_B` (peft's `.lora_A.<adapter>` too) or kohya's
+ * `lora_unet_<flattened>.lora_down` / `.lora_up`; an alpha (per module, or in
+ * the file's metadata) folds alpha / rank into the delta. A name bound at the
+ * wrong shape refuses the WHOLE slot; a slot that binds nothing is reported
+ * loudly. Neither is an error: the base model runs. */
+typedef struct ming_lora_spec {
+  const char* path;
+  float scale;
+} ming_lora_spec;
+/* The projections an adapter may bind: 7 x (2 * n_refiner + n_layers). */
+int ming_lora_module_capacity(const ming_dit_config* cfg);
+/* MingDit::load from a directory: config refusals (cfg_from_), shape checks,
+ * every weight resident (quantized or dense as the checkpoint holds it), the
+ * adapters bound. The model owns everything it loaded. */
+int ming_model_load(ming_ctx* ctx, const char* transformer_dir, const ming_lora_spec* loras,
+                    int n_loras, ming_model** out);
+/* Binds adapter files to a model's projections (a loaded model, or one made by
+ * ming_model_create, whose borrowed weights then carry the bindings). A slot a
+ * spec names is unbound first; its strength is set to the spec's scale. */
+int ming_model_bind_loras(ming_model* m, const ming_lora_spec* loras, int n_loras);
+/* Projections slot `slot` bound; modules refused at the wrong shape; the
+ * binding report (what the log said). */
+int ming_model_lora_modules(const ming_model* m, int slot);
+int ming_model_lora_skipped(const ming_model* m, int slot);
+const char* ming_model_lora_report(const ming_model* m, int slot);
 
 #ifdef __cplusplus
 }

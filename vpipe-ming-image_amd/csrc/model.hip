@@ -14,12 +14,14 @@
 //     reference's _fold_mod path, 1602-1606): nw = norm_w * (1 + scale).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
 #include <string>
 #include <vector>
 
+#include "model.h"
 #include "rt.h"
 
 namespace {
@@ -147,23 +149,6 @@ uint16_t host_bf16(float f) {
 
 }  // namespace
 
-struct ming_model {
-  ming_ctx* ctx = nullptr;
-  ming_model_desc d{};
-  std::vector<ming_block_desc> ctx_blocks, blocks;
-  float scales[MING_MAX_LORA_SLOTS] = {};
-  // per-forward device planes, grown on demand
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
-  int ws_rows = -1, ws_q = -1;
-  uint16_t *joint = nullptr, *capn = nullptr, *tin = nullptr, *te1 = nullptr,
-           *temb = nullptr, *tsilu = nullptr, *outmod = nullptr;
-  float *cos_t = nullptr, *sin_t = nullptr;
-  int32_t* pos = nullptr;
-  void* blk_ws = nullptr;
-  size_t blk_bytes = 0;
-  std::vector<uint16_t> tin_host;
-};
 
 namespace {
 
@@ -204,7 +189,185 @@ int ensure_model_ws(ming_model* m, int JT, int Q) {
   return MING_OK;
 }
 
+// flag = 1 when the n bytes (n % 16 == 0, both 16-byte aligned) differ.
+__global__ void bytes_differ_kernel(const uint4* a, const uint4* b, size_t n16, int* flag) {
+  bool diff = false;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const uint4 x = a[i], y = b[i];
+    diff |= (x.x != y.x) | (x.y != y.y) | (x.z != y.z) | (x.w != y.w);
+  }
+  if (diff) *flag = 1;  // every writer stores the same value
+}
+
+void free_cap_entry(ming_model::CapEntry& e) {
+  if (e.key) (void)hipFree(e.key);
+  if (e.out) (void)hipFree(e.out);
+  e = ming_model::CapEntry{};
+}
+
+// Grows a device buffer to `bytes` (contents not kept). false when it cannot.
+bool grow(void** p, size_t* cap, size_t bytes) {
+  if (*cap >= bytes && *p) return true;
+  if (*p) (void)hipFree(*p);
+  *p = nullptr;
+  *cap = 0;
+  if (hipMalloc(p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    *p = nullptr;
+    return false;
+  }
+  *cap = bytes;
+  return true;
+}
+
+// The caption-cache entry holding exactly these caption bytes, or null
+// (ming-dit.cc:1543-1560): shape fields first, then the bytes, compared on
+// the device.
+int cap_lookup(ming_model* m, const uint16_t* cap, int CAP, int Q, int64_t stride,
+               hipStream_t s, ming_model::CapEntry** hit) {
+  *hit = nullptr;
+  const size_t bytes = (size_t)CAP * (size_t)stride * 2;
+  int cand[2], nc = 0;
+  for (int i = 0; i < 2; ++i) {
+    const ming_model::CapEntry& e = m->cap[i];
+    if (e.valid && e.q == Q && e.len == CAP && e.stride == stride && e.key_bytes == bytes)
+      cand[nc++] = i;
+  }
+  if (nc == 0) return MING_OK;
+  if (!m->cap_flag) {
+    if (hipMalloc(&m->cap_flag, 2 * sizeof(int)) != hipSuccess) {
+      (void)hipGetLastError();
+      m->cap_flag = nullptr;
+      return MING_OK;  // no comparison, no hit: the caption path runs
+    }
+  }
+  if (hipMemsetAsync(m->cap_flag, 0, 2 * sizeof(int), s) != hipSuccess)
+    return rt_fail(MING_ERR_HIP, "ming_model_forward: caption cache flag reset failed");
+  const size_t n16 = bytes / 16;
+  const unsigned grid = (unsigned)std::min<size_t>((n16 + 255) / 256, 1024);
+  for (int k = 0; k < nc; ++k) {
+    hipLaunchKernelGGL(bytes_differ_kernel, dim3(grid > 0 ? grid : 1), dim3(256), 0, s,
+                       static_cast<const uint4*>(m->cap[cand[k]].key),
+                       reinterpret_cast<const uint4*>(cap), n16, m->cap_flag + k);
+    if (hipGetLastError() != hipSuccess)
+      return rt_fail(MING_ERR_HIP, "ming_model_forward: caption compare launch failed");
+  }
+  int differ[2] = {1, 1};
+  if (hipMemcpyAsync(differ, m->cap_flag, 2 * sizeof(int), hipMemcpyDeviceToHost, s) !=
+          hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return rt_fail(MING_ERR_HIP, "ming_model_forward: caption compare failed");
+  for (int k = 0; k < nc; ++k)
+    if (!differ[k]) {
+      *hit = &m->cap[cand[k]];
+      break;
+    }
+  return MING_OK;
+}
+
+// Block progress (set_block_progress): report k goes out once blocks [0, k)
+// have finished, in order, each k once, on the calling thread.
+struct Progress {
+  ming_model* m = nullptr;
+  int total = 0, recorded = 0, reported = 0;
+  bool on() const { return m && m->progress; }
+  int init(ming_model* mm, int n) {
+    m = mm;
+    total = n;
+    if (!on()) return MING_OK;
+    while ((int)m->block_events.size() < n) {
+      hipEvent_t e;
+      if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
+        return rt_fail(MING_ERR_HIP, "ming_model_forward: progress event creation failed");
+      m->block_events.push_back(static_cast<void*>(e));
+    }
+    return MING_OK;
+  }
+  int done_block(hipStream_t s) {
+    if (!on()) return MING_OK;
+    if (hipEventRecord(static_cast<hipEvent_t>(m->block_events[(size_t)recorded]), s) !=
+        hipSuccess)
+      return rt_fail(MING_ERR_HIP, "ming_model_forward: progress event record failed");
+    ++recorded;
+    return MING_OK;
+  }
+  void poll(bool wait) {
+    if (!on()) return;
+    while (reported < total && reported <= recorded) {
+      if (reported > 0) {
+        hipEvent_t e = static_cast<hipEvent_t>(m->block_events[(size_t)reported - 1]);
+        if (wait) {
+          if (hipEventSynchronize(e) != hipSuccess) return;
+        } else if (hipEventQuery(e) != hipSuccess) {
+          (void)hipGetLastError();  // "not ready" is not an error to keep
+          return;
+        }
+      }
+      m->progress(m->progress_user, reported, total);
+      ++reported;
+    }
+  }
+};
+
+// A cooperative stop: the queued work drains, the forward reports MING_STOPPED
+// with no error (ming-dit.h:170-189).
+bool stop_requested(ming_model* m) { return m->stop && m->stop(m->stop_user) != 0; }
+int stopped(hipStream_t s) {
+  (void)hipStreamSynchronize(s);
+  ming::rt_ok();
+  return MING_STOPPED;
+}
+
+// Whether `slot` is bound on any context-refiner projection: only then does a
+// strength change touch the cached caption rows (ming-dit.cc:3031-3038).
+bool slot_in_ctx_refiner(const ming_model* m, int slot) {
+  for (const ming_block_desc& b : m->ctx_blocks)
+    for (const ming_qweight* q : {b.q, b.k, b.v, b.o, b.w1, b.w3, b.w2}) {
+      int N = 0, K = 0, ns = 0;
+      if (!q || ming_qweight_shape(q, &N, &K, &ns) != MING_OK) continue;
+      for (int sg = 0; sg < ns; ++sg)
+        if (ming_qweight_lora_rank(q, sg, slot) > 0) return true;
+    }
+  return false;
+}
+
 }  // namespace
+
+namespace ming {
+
+std::vector<ModuleRef> model_modules(const ming_model* m) {
+  std::vector<ModuleRef> v;
+  const ming_model_desc& d = m->d;
+  const int H = d.hidden, F = d.ffn;
+  auto one = [&](const std::string& pre, const ming_block_desc& b, bool ctx) {
+    const struct {
+      const char* nm;
+      const ming_qweight* q;
+      int N, K;
+    } p[7] = {{"attention.to_q", b.q, H, H},        {"attention.to_k", b.k, H, H},
+              {"attention.to_v", b.v, H, H},        {"attention.to_out.0", b.o, H, H},
+              {"feed_forward.w1", b.w1, F, H},      {"feed_forward.w3", b.w3, F, H},
+              {"feed_forward.w2", b.w2, H, F}};
+    for (const auto& x : p)
+      v.push_back({pre + x.nm, const_cast<ming_qweight*>(x.q), x.N, x.K, ctx});
+  };
+  for (int L = 0; L < (int)m->blocks.size(); ++L) {
+    const std::string pre = L < d.n_refiner
+                                ? "noise_refiner." + std::to_string(L) + "."
+                                : "layers." + std::to_string(L - d.n_refiner) + ".";
+    one(pre, m->blocks[(size_t)L], false);
+  }
+  for (int i = 0; i < (int)m->ctx_blocks.size(); ++i)
+    one("context_refiner." + std::to_string(i) + ".", m->ctx_blocks[(size_t)i], true);
+  return v;
+}
+
+void model_drop_caption_cache(ming_model* m) {
+  for (auto& e : m->cap) e.valid = false;
+}
+
+}  // namespace ming
 
 extern "C" {
 
@@ -283,8 +446,37 @@ int ming_model_destroy(ming_model* m) {
   if (!m) return rt_ok();
   (void)hipStreamSynchronize((hipStream_t)ming_ctx_stream(m->ctx));
   if (m->ws) (void)hipFree(m->ws);
+  for (auto& e : m->cap) free_cap_entry(e);
+  if (m->cap_flag) (void)hipFree(m->cap_flag);
+  for (void* e : m->block_events) (void)hipEventDestroy(static_cast<hipEvent_t>(e));
+  for (ming_qweight* q : m->own_qw) (void)ming_qweight_destroy(q);
+  for (void* p : m->own_dev) ming::rt_free(m->ctx, p);
   ming::rt_release(m->ctx);
   delete m;
+  return rt_ok();
+}
+
+int ming_model_set_stream_stop(ming_model* m, ming_stop_fn fn, void* user) {
+  if (!m) return rt_fail(MING_ERR_ARG, "ming_model_set_stream_stop: null model");
+  m->stop = fn;
+  m->stop_user = user;
+  return rt_ok();
+}
+
+int ming_model_set_block_progress(ming_model* m, ming_progress_fn fn, void* user) {
+  if (!m) return rt_fail(MING_ERR_ARG, "ming_model_set_block_progress: null model");
+  m->progress = fn;
+  m->progress_user = user;
+  return rt_ok();
+}
+
+int ming_model_set_caption_cache(ming_model* m, int on) {
+  if (!m) return rt_fail(MING_ERR_ARG, "ming_model_set_caption_cache: null model");
+  m->cap_cache_on = on != 0;
+  if (!m->cap_cache_on) {
+    (void)hipStreamSynchronize((hipStream_t)ming_ctx_stream(m->ctx));
+    for (auto& e : m->cap) free_cap_entry(e);
+  }
   return rt_ok();
 }
 
@@ -294,7 +486,10 @@ int ming_model_set_lora_scale(ming_model* m, int slot, float s) {
     return rt_fail(MING_ERR_ARG, "ming_model_set_lora_scale: slot out of range");
   if (!std::isfinite(s))
     return rt_fail(MING_ERR_ARG, "ming_model_set_lora_scale: strength must be finite");
+  if (m->scales[slot] == s) return rt_ok();
   m->scales[slot] = s;
+  // the cached caption rows were refined at the old strength
+  if (slot_in_ctx_refiner(m, slot)) ming::model_drop_caption_cache(m);
   return rt_ok();
 }
 
@@ -363,9 +558,40 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
   RC(ming_silu(c, m->temb, m->tsilu, d.adaln_dim));
   // embeddings: image rows through x_embedder; caption query rows through
   // cap_embedder (RMSNorm + Linear), the rest copied (2283-2304)
+  // the caption cache (ming-dit.cc:1543-1577): a hit serves the whole caption
+  // path; a miss refills an empty entry, else the least recently used one,
+  // which becomes valid only when this forward completes
+  ming_model::CapEntry* hit = nullptr;
+  ming_model::CapEntry* fill = nullptr;
+  const size_t cap_bytes = (size_t)CAP * (size_t)cap_stride * 2;
+  const bool cacheable = m->cap_cache_on && reinterpret_cast<uintptr_t>(cap) % 16 == 0;
+  if (cacheable) {
+    RC(cap_lookup(m, cap, CAP, Q, cap_stride, s, &hit));
+    if (!hit) {
+      fill = &m->cap[0];
+      for (auto& e : m->cap) {
+        if (!e.valid) {
+          fill = &e;
+          break;
+        }
+        if (e.tick < fill->tick) fill = &e;
+      }
+      fill->valid = false;
+      if (!grow(&fill->key, &fill->key_cap, cap_bytes) ||
+          !grow(&fill->out, &fill->out_cap, (size_t)CAP * H * 2))
+        fill = nullptr;  // no room: this forward runs uncached
+    }
+  }
   RC(ming_lin(c, d.x_in, latents, d.patch_dim, m->joint, H, IMG, nullptr));
   RC(ming_bias_act(c, m->joint, H, d.x_in_b, IMG, H, 0));
   uint16_t* cap0 = m->joint + (size_t)IMG * H;
+  if (hit) {
+    if (hipMemcpyAsync(cap0, hit->out, (size_t)CAP * H * 2, hipMemcpyDeviceToDevice, s) !=
+        hipSuccess)
+      return rt_fail(MING_ERR_HIP, "ming_model_forward: caption cache copy failed");
+    hit->tick = ++m->cap_tick;
+    ming::rt_note_cap_hit(c);
+  } else {
   if (Q > 0) {
     if (hipMemcpy2DAsync(m->capn, (size_t)d.cap_dim * 2, cap, (size_t)cap_stride * 2,
                          (size_t)d.cap_dim * 2, Q, hipMemcpyDeviceToDevice, s) != hipSuccess)
@@ -380,19 +606,46 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
                        (size_t)cap_stride * 2, (size_t)H * 2, CAP - Q,
                        hipMemcpyDeviceToDevice, s) != hipSuccess)
     return rt_fail(MING_ERR_HIP, "ming_model_forward: caption copy failed");
+  }
   // blocks: the context refiner over the caption rows (its table rows start
   // at IMG), then the noise refiner over the image rows and the main layers
-  // over the joint sequence
+  // over the joint sequence; stop polled and progress reported per block
   ming_block_dims bd{d.hidden, d.n_heads, d.ffn, d.adaln_dim, d.eps};
   BlockWs w{};
   block_ws_layout(bd, JT, static_cast<char*>(m->blk_ws), &w);
-  for (int i = 0; i < d.n_refiner; ++i)
-    RC(block_forward(c, &m->ctx_blocks[(size_t)i], bd, cap0, CAP, m->cos_t + (size_t)IMG * 64,
-                     m->sin_t + (size_t)IMG * 64, nullptr, m->scales, w));
-  for (int L = 0; L < d.n_refiner + d.n_layers; ++L) {
+  const int NM = d.n_refiner + d.n_layers;
+  Progress prog;
+  RC(prog.init(m, d.n_refiner + NM));
+  for (int i = 0; i < d.n_refiner; ++i) {
+    if (stop_requested(m)) return stopped(s);
+    prog.poll(false);
+    if (!hit)
+      RC(block_forward(c, &m->ctx_blocks[(size_t)i], bd, cap0, CAP,
+                       m->cos_t + (size_t)IMG * 64, m->sin_t + (size_t)IMG * 64, nullptr,
+                       m->scales, w));
+    RC(prog.done_block(s));
+  }
+  if (fill) {
+    // before the main stack rewrites these rows in place
+    if (hipMemcpyAsync(fill->out, cap0, (size_t)CAP * H * 2, hipMemcpyDeviceToDevice, s) !=
+            hipSuccess ||
+        hipMemcpyAsync(fill->key, cap, cap_bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return rt_fail(MING_ERR_HIP, "ming_model_forward: caption cache fill failed");
+  }
+  for (int L = 0; L < NM; ++L) {
+    if (stop_requested(m)) return stopped(s);
+    prog.poll(false);
     const int rows = L < d.n_refiner ? IMG : JT;
     RC(block_forward(c, &m->blocks[(size_t)L], bd, m->joint, rows, m->cos_t, m->sin_t,
                      m->temb, m->scales, w));
+    RC(prog.done_block(s));
+    // with a stop wired, the host stays within 4 blocks of the GPU so that a
+    // stop requested mid-forward is seen (ming-dit.cc:2530-2540)
+    if (m->stop && (L + 1) % 4 == 0 && L + 1 < NM) {
+      if (hipStreamSynchronize(s) != hipSuccess)
+        return rt_fail(MING_ERR_HIP, "ming_model_forward: the GPU failed");
+      prog.poll(false);
+    }
   }
   // final layer: adaLN scale from silu(temb), LayerNorm (eps 1e-6) + modulate,
   // then the linear to the patch dimension (2557-2563)
@@ -401,8 +654,17 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
   RC(ming_ln_modulate(c, m->joint, H, m->outmod, w.nrm, H, IMG, H, 1e-6f));
   RC(ming_lin(c, d.final_lin, w.nrm, H, out, d.patch_dim, IMG, nullptr));
   RC(ming_bias_act(c, out, d.patch_dim, d.final_lin_b, IMG, d.patch_dim, 0));
+  prog.poll(true);
   if (hipStreamSynchronize(s) != hipSuccess)
     return rt_fail(MING_ERR_HIP, "ming_model_forward: the GPU failed");
+  if (fill) {
+    fill->valid = true;
+    fill->q = Q;
+    fill->len = CAP;
+    fill->stride = cap_stride;
+    fill->key_bytes = cap_bytes;
+    fill->tick = ++m->cap_tick;
+  }
   return rt_ok();
 }
 

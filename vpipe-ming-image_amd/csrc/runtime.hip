@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -22,6 +23,11 @@
 namespace {
 
 thread_local std::string g_err;
+
+// The process-wide session log (ming_set_log_sink).
+std::mutex g_log_mu;
+ming_log_fn g_log_fn = nullptr;
+void* g_log_user = nullptr;
 
 int fail(int code, const std::string& why) {
   g_err = why;
@@ -340,6 +346,12 @@ extern "C" {
 
 const char* ming_last_error(void) { return g_err.c_str(); }
 int ming_abi_version(void) { return MING_ABI_VERSION; }
+
+void ming_set_log_sink(ming_log_fn fn, void* user) {
+  std::lock_guard<std::mutex> g(g_log_mu);
+  g_log_fn = fn;
+  g_log_user = user;
+}
 
 int ming_ctx_create(int device, void* hip_stream, ming_ctx** out) {
   if (!out) return fail(MING_ERR_ARG, "ming_ctx_create: null out");
@@ -1219,4 +1231,40 @@ int rt_ok() { return ok(); }
 int rt_device(const ming_ctx* c) { return c ? c->device : -1; }
 void rt_retain(ming_ctx* c) { c->live_weights += 1; }
 void rt_release(ming_ctx* c) { c->live_weights -= 1; }
+
+void rt_log(int level, const std::string& msg) {
+  ming_log_fn fn;
+  void* user;
+  {
+    std::lock_guard<std::mutex> g(g_log_mu);
+    fn = g_log_fn;
+    user = g_log_user;
+  }
+  if (fn) fn(user, level, msg.c_str());
+}
+
+int rt_upload(ming_ctx* c, const void* host, size_t bytes, void** dev) {
+  *dev = nullptr;
+  if (bytes == 0) return ok();
+  DeviceGuard dg(c->device);
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MING_ERR_ALLOC, "device allocation of " + std::to_string(bytes) + " bytes failed");
+  }
+  if (hipMemcpy(p, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(p);
+    return fail(MING_ERR_HIP, "host to device copy failed");
+  }
+  *dev = p;
+  return ok();
+}
+
+void rt_free(ming_ctx* c, void* dev) {
+  if (!dev) return;
+  DeviceGuard dg(c->device);
+  (void)hipFree(dev);
+}
+
+void rt_note_cap_hit(ming_ctx* c) { c->eng.cap_cache_hits += 1; }
 }  // namespace ming

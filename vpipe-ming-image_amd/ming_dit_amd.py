@@ -34,7 +34,8 @@ class Engagement(C.Structure):
                 ("lora_xa", C.c_int64), ("rmsnorm", C.c_int64),
                 ("qk_norm_rope", C.c_int64), ("rope_table", C.c_int64),
                 ("attention", C.c_int64), ("elementwise", C.c_int64),
-                ("gemm_flops", C.c_uint64), ("gemm_fast", C.c_int64)]
+                ("gemm_flops", C.c_uint64), ("gemm_fast", C.c_int64),
+                ("cap_cache_hits", C.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -72,6 +73,38 @@ class ModelDesc(C.Structure):
                    ("time_1", "time_1b", "time_2", "time_2b", "x_in",
                     "x_in_b", "cap_norm", "cap_in", "cap_in_b", "final_ada",
                     "final_ada_b", "final_lin", "final_lin_b")])
+
+
+class DitConfig(C.Structure):
+    """ming_dit_config: transformer/config.json as the loader read it."""
+    _fields_ = ([(n, C.c_int) for n in
+                 ("dim", "n_layers", "n_refiner_layers", "n_heads",
+                  "n_kv_heads", "in_channels", "patch", "f_patch",
+                  "cap_feat_dim", "qk_norm")]
+                + [("norm_eps", C.c_float), ("rope_theta", C.c_float),
+                   ("t_scale", C.c_float), ("axes_dims", C.c_int * 3),
+                   ("axes_lens", C.c_int * 3)]
+                + [(n, C.c_int) for n in
+                   ("zero_masked", "multi_frame_output", "ffn_inner",
+                    "adaln_dim", "time_mid", "time_freq", "patch_dim")])
+
+    def as_dict(self):
+        out = {}
+        for k, _ in self._fields_:
+            v = getattr(self, k)
+            out[k] = list(v) if isinstance(v, C.Array) else v
+        return out
+
+
+class LoraSpec(C.Structure):
+    _fields_ = [("path", C.c_char_p), ("scale", C.c_float)]
+
+
+LOG_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_char_p)
+STOP_FN = C.CFUNCTYPE(C.c_int, C.c_void_p)
+PROGRESS_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_int)
+STOPPED = -1
+LOG_WARN, LOG_INFO = 1, 2
 
 
 def lib():
@@ -142,6 +175,28 @@ def lib():
         "ming_model_forward": ([vp, vp, vp, i64, i32, i32, i32,
                                 C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                 C.POINTER(C.c_int32), f32, vp], i32),
+        "ming_set_log_sink": ([LOG_FN, vp], None),
+        "ming_model_set_stream_stop": ([vp, STOP_FN, vp], i32),
+        "ming_model_set_block_progress": ([vp, PROGRESS_FN, vp], i32),
+        "ming_model_set_caption_cache": ([vp, i32], i32),
+        "ming_pack_open": ([C.c_char_p, C.POINTER(vp)], i32),
+        "ming_pack_close": ([vp], i32),
+        "ming_pack_config": ([vp, C.POINTER(DitConfig)], i32),
+        "ming_pack_quant_bits": ([vp], i32),
+        "ming_pack_group": ([vp], i32),
+        "ming_pack_tensor_count": ([vp], i32),
+        "ming_pack_tensor_name": ([vp, i32], C.c_char_p),
+        "ming_pack_tensor_info": ([vp, C.c_char_p, C.c_char_p,
+                                   C.POINTER(i64), C.POINTER(i32)], i32),
+        "ming_pack_quantized_count": ([vp], i32),
+        "ming_pack_write": ([C.c_char_p, C.c_char_p, i32, i32], i32),
+        "ming_lora_module_capacity": ([C.POINTER(DitConfig)], i32),
+        "ming_model_load": ([vp, C.c_char_p, C.POINTER(LoraSpec), i32,
+                             C.POINTER(vp)], i32),
+        "ming_model_bind_loras": ([vp, C.POINTER(LoraSpec), i32], i32),
+        "ming_model_lora_modules": ([vp, i32], i32),
+        "ming_model_lora_skipped": ([vp, i32], i32),
+        "ming_model_lora_report": ([vp, i32], C.c_char_p),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -431,23 +486,142 @@ def block_desc(**parts) -> BlockDesc:
     return d
 
 
-class Model:
-    """ming_model over borrowed weights: the caller keeps every QWeight and
-    tensor in `desc` alive for the model's lifetime (held here too)."""
+_log_keep = None
 
-    def __init__(self, ctx: Ctx, desc: ModelDesc, ctx_blocks, blocks,
-                 keep=()):
-        self.ctx = ctx
-        self._cb = (BlockDesc * max(len(ctx_blocks), 1))(*ctx_blocks)
-        self._mb = (BlockDesc * max(len(blocks), 1))(*blocks)
-        desc.ctx_blocks = C.cast(self._cb, C.POINTER(BlockDesc))
-        desc.blocks = C.cast(self._mb, C.POINTER(BlockDesc))
-        self.desc = desc
-        self._keep = list(keep)
+
+def set_log_sink(fn=None):
+    """Route the library's session log to fn(level, message) (None: drop)."""
+    global _log_keep
+    if fn is None:
+        _log_keep = None
+        lib().ming_set_log_sink(LOG_FN(), None)
+        return
+    cb = LOG_FN(lambda _u, level, msg: fn(int(level),
+                                           msg.decode(errors="replace")))
+    _log_keep = cb
+    lib().ming_set_log_sink(cb, None)
+
+
+def _specs(loras):
+    """[(path or None, scale), ...] -> (LoraSpec array, n, keep)."""
+    loras = list(loras or [])
+    arr = (LoraSpec * max(len(loras), 1))()
+    keep = []
+    for i, (path, scale) in enumerate(loras):
+        b = os.fsencode(path) if path else None
+        keep.append(b)
+        arr[i].path = b
+        arr[i].scale = float(scale)
+    return arr, len(loras), keep
+
+
+class Pack:
+    """A transformer directory opened by ming_pack_open (config + tensors)."""
+
+    def __init__(self, transformer_dir: str):
         h = C.c_void_p()
-        _check(lib().ming_model_create(ctx.h, C.byref(desc), C.byref(h)))
+        _check(lib().ming_pack_open(os.fsencode(transformer_dir), C.byref(h)))
         self.h = h
+
+    def config(self) -> dict:
+        c = DitConfig()
+        _check(lib().ming_pack_config(self.h, C.byref(c)))
+        return c.as_dict()
+
+    def config_struct(self) -> DitConfig:
+        c = DitConfig()
+        _check(lib().ming_pack_config(self.h, C.byref(c)))
+        return c
+
+    @property
+    def quant_bits(self) -> int:
+        return int(lib().ming_pack_quant_bits(self.h))
+
+    @property
+    def group(self) -> int:
+        return int(lib().ming_pack_group(self.h))
+
+    def names(self) -> list:
+        n = lib().ming_pack_tensor_count(self.h)
+        return [lib().ming_pack_tensor_name(self.h, i).decode() for i in range(n)]
+
+    def info(self, name: str):
+        dt = C.create_string_buffer(8)
+        shape = (C.c_int64 * 8)()
+        nd = C.c_int()
+        _check(lib().ming_pack_tensor_info(self.h, name.encode(), dt, shape,
+                                           C.byref(nd)))
+        return dt.value.decode(), tuple(shape[i] for i in range(nd.value))
+
+    def quantized_count(self) -> int:
+        return int(lib().ming_pack_quantized_count(self.h))
+
+    def close(self):
+        if self.h:
+            lib().ming_pack_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def pack_write(src_dir: str, dst_dir: str, bits: int, threads: int = 0):
+    _check(lib().ming_pack_write(os.fsencode(src_dir), os.fsencode(dst_dir),
+                                 int(bits), int(threads)))
+
+
+def lora_module_capacity(cfg: DitConfig) -> int:
+    return int(lib().ming_lora_module_capacity(C.byref(cfg)))
+
+
+class Model:
+    """ming_model. Made over borrowed weights (the caller keeps every QWeight
+    and tensor in `desc` alive for the model's lifetime; held here too), or
+    loaded from a transformer directory with Model.load (the model owns what
+    it loaded)."""
+
+    def __init__(self, ctx: Ctx, desc: ModelDesc | None, ctx_blocks=(),
+                 blocks=(), keep=(), _handle=None):
+        self.ctx = ctx
+        self._cbs = {}
+        self._keep = list(keep)
+        if _handle is not None:
+            self.desc = None
+            self.h = _handle
+        else:
+            self._cb = (BlockDesc * max(len(ctx_blocks), 1))(*ctx_blocks)
+            self._mb = (BlockDesc * max(len(blocks), 1))(*blocks)
+            desc.ctx_blocks = C.cast(self._cb, C.POINTER(BlockDesc))
+            desc.blocks = C.cast(self._mb, C.POINTER(BlockDesc))
+            self.desc = desc
+            h = C.c_void_p()
+            _check(lib().ming_model_create(ctx.h, C.byref(desc), C.byref(h)))
+            self.h = h
         ctx._weights.add(self)
+
+    @classmethod
+    def load(cls, ctx: Ctx, transformer_dir: str, loras=None) -> "Model":
+        arr, n, keep = _specs(loras)
+        h = C.c_void_p()
+        _check(lib().ming_model_load(ctx.h, os.fsencode(transformer_dir), arr,
+                                     n, C.byref(h)))
+        return cls(ctx, None, _handle=h)
+
+    def bind_loras(self, loras):
+        arr, n, keep = _specs(loras)
+        _check(lib().ming_model_bind_loras(self.h, arr, n))
+
+    def lora_modules(self, slot: int) -> int:
+        return int(lib().ming_model_lora_modules(self.h, slot))
+
+    def lora_skipped(self, slot: int) -> int:
+        return int(lib().ming_model_lora_skipped(self.h, slot))
+
+    def lora_report(self, slot: int) -> str:
+        return lib().ming_model_lora_report(self.h, slot).decode(errors="replace")
 
     def set_lora_scale(self, slot: int, s: float):
         _check(lib().ming_model_set_lora_scale(self.h, slot, float(s)))
@@ -455,16 +629,37 @@ class Model:
     def lora_scale(self, slot: int) -> float:
         return float(lib().ming_model_lora_scale(self.h, slot))
 
+    def set_stream_stop(self, fn=None):
+        """fn() -> bool, polled before every block (None clears it)."""
+        cb = STOP_FN(lambda _u: 1 if fn() else 0) if fn else STOP_FN()
+        self._cbs["stop"] = cb
+        _check(lib().ming_model_set_stream_stop(self.h, cb, None))
+
+    def set_block_progress(self, fn=None):
+        """fn(done, total) once per block, in order (None clears it)."""
+        cb = (PROGRESS_FN(lambda _u, d, t: fn(int(d), int(t))) if fn
+              else PROGRESS_FN())
+        self._cbs["progress"] = cb
+        _check(lib().ming_model_set_block_progress(self.h, cb, None))
+
+    def set_caption_cache(self, on: bool):
+        _check(lib().ming_model_set_caption_cache(self.h, int(bool(on))))
+
     def forward(self, latents, cap, cap_stride: int, img_tokens: int,
                 cap_len: int, query_rows: int, pos_t, pos_h, pos_w,
-                sigma: float, out):
+                sigma: float, out) -> bool:
+        """True when the forward ran, False on a cooperative stop."""
         import numpy as np
         arrs = [np.ascontiguousarray(a, np.int32) for a in (pos_t, pos_h, pos_w)]
         ptrs = [a.ctypes.data_as(C.POINTER(C.c_int32)) for a in arrs]
-        _check(lib().ming_model_forward(self.h, _ptr(latents), _ptr(cap),
-                                        cap_stride, img_tokens, cap_len,
-                                        query_rows, *ptrs, float(sigma),
-                                        _ptr(out)))
+        rc = lib().ming_model_forward(self.h, _ptr(latents), _ptr(cap),
+                                      cap_stride, img_tokens, cap_len,
+                                      query_rows, *ptrs, float(sigma),
+                                      _ptr(out))
+        if rc == STOPPED:
+            return False
+        _check(rc)
+        return True
 
     def close(self):
         if self.h:
