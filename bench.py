@@ -248,6 +248,51 @@ def time_forward(ctx, m, torch, gen, steps, warmup):
     return ms, flops
 
 
+def time_norms(ctx, torch, gen, reps=20):
+    """The HBM-bound feeds at configs[3]'s shape (4352 rows, H 3840, 30 heads):
+    RMSNorm [4352, 3840] out of place, and qk-norm + RoPE in place on the
+    token-major [4352, 3*3840] qkv plane. Per-launch HIP events; achieved =
+    algorithmic bytes (activations read + written once, gains; the rotary
+    tables excluded) / average launch time, against 8 TB/s."""
+    import numpy as np
+    rows, H, NH = M_TOK, HID, HID // 128
+    x = torch.randn((rows, H), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    y = torch.empty_like(x)
+    w = (1.0 + 0.1 * torch.randn((H,), generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
+    qkv = torch.randn((rows, 3 * H), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    nq = (1.0 + 0.1 * torch.randn((128,), generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
+    nk = (1.0 + 0.1 * torch.randn((128,), generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
+    img, cap, grid = 4096, 256, 64
+    pt = torch.from_numpy(np.concatenate([np.full(img, cap + 1), 1 + np.arange(cap)]).astype(np.int32)).cuda()
+    ph = torch.from_numpy(np.concatenate([np.arange(img) // grid, np.zeros(cap)]).astype(np.int32)).cuda()
+    pw = torch.from_numpy(np.concatenate([np.arange(img) % grid, np.zeros(cap)]).astype(np.int32)).cuda()
+    cos_t = torch.empty((rows, 64), dtype=torch.float32, device="cuda")
+    sin_t = torch.empty_like(cos_t)
+    ctx.rope_table(pt, ph, pw, rows, cos_t, sin_t)
+    for _ in range(3):
+        ctx.rmsnorm(x, w, y, rows, H)
+        ctx.qk_norm_rope(qkv, 3 * H, 0, H, rows, NH, nq, nk, cos_t, sin_t)
+    ctx.synchronize()
+    ctx.set_profiling(True)
+    ctx.profile_collect()
+    for _ in range(reps):
+        ctx.rmsnorm(x, w, y, rows, H)
+        ctx.qk_norm_rope(qkv, 3 * H, 0, H, rows, NH, nq, nk, cos_t, sin_t)
+    ctx.synchronize()
+    prof = ctx.profile_collect()
+    ctx.set_profiling(False)
+    out = {}
+    for k, shape in (("rmsnorm", [rows, H]), ("qk_norm_rope", [rows, 2 * H])):
+        b = prof[k]
+        gbps = b["bytes"] / (b["ms"] * 1e-3) / 1e9
+        out[k] = {"shape": shape, "launches": b["launches"],
+                  "avg_us": round(1e3 * b["ms"] / b["launches"], 2),
+                  "bytes_per_launch": round(b["bytes"] / b["launches"]),
+                  "achieved_gbps": round(gbps, 1), "peak_gbps": 8000.0,
+                  "frac": round(gbps / 8000.0, 4)}
+    return out
+
+
 TRAFFIC_MD = os.path.join(ROOT, "profiles", "qproj_w4_ffn_config2_traffic.md")
 
 
@@ -385,6 +430,7 @@ def main():
     }
     for w in (w1, w3, w2):
         w.close()
+    out["hbm_kernels"] = time_norms(ctx, torch, gen)
     if not args.no_forward:
         fms, fflops = time_forward(ctx, m, torch, gen, args.forward_steps, 1)
         out["forward_ms_1024"] = round(fms, 2)

@@ -175,3 +175,66 @@ def test_block_config3_full_size(ctx):
         for slot in range(8):
             parts[n].unbind_lora(slot)
     assert np.array_equal(z, run(desc, [0.0] * 8))
+
+
+def public_block(ctx, gp, x, rows, c, s, temb, scales, modulated):
+    """run_block's attention half and the feed-forward pre-norm composed from
+    the public entry points one by one (each projection converting its own
+    input, the post-norm in place, then the residual kernel): the sequence
+    the block driver fuses."""
+    import torch
+    Hh = H
+    xd = to_dev(x)
+    cd, sd = to_dev(np.ascontiguousarray(c)), to_dev(np.ascontiguousarray(s))
+    dev = lambda *sh: torch.empty(sh, dtype=torch.int16, device="cuda")
+    nrm, qkv, ob, ffg = dev(rows, Hh), dev(rows, 3 * Hh), dev(rows, Hh), dev(rows, F)
+    g1, g3 = gp["an1"], gp["fn1"]
+    if modulated:
+        mods, nw1, nw3 = dev(1, 4 * Hh), dev(1, Hh), dev(1, Hh)
+        ctx.lin(gp["ada"], to_dev(temb), mods, 1, None)
+        ctx.bias_act(mods, gp["ada_b"], 1, 4 * Hh)
+        ctx.modulate(gp["an1"], mods, nw1, 1, Hh)
+        ctx.modulate(gp["fn1"], mods[:, 2 * Hh:], nw3, 1, Hh)
+        g1, g3 = nw1, nw3
+    sync()
+    ctx.rmsnorm(xd, g1, nrm, rows, Hh)
+    ctx.lin(gp["q"], nrm, qkv, rows, scales, ldy=3 * Hh)
+    ctx.lin(gp["k"], nrm, qkv[:, Hh:], rows, scales, ldy=3 * Hh)
+    ctx.lin(gp["v"], nrm, qkv[:, 2 * Hh:], rows, scales, ldy=3 * Hh)
+    ctx.qk_norm_rope(qkv, 3 * Hh, 0, Hh, rows, NH, gp["nq"], gp["nk"], cd, sd)
+    ctx.attention(qkv, 3 * Hh, 0, Hh, 2 * Hh, nrm, Hh, rows, NH, 1.0 / np.sqrt(128.0))
+    ctx.lin(gp["o"], nrm, ob, rows, scales)
+    ctx.rmsnorm(ob, gp["an2"], ob, rows, Hh)
+    if modulated:
+        ctx.gated_residual(xd, mods[:, Hh:], ob, rows, Hh)
+    else:
+        ctx.residual_add(xd, ob, rows, Hh)
+    ctx.rmsnorm(xd, g3, nrm, rows, Hh)
+    return xd, nrm, qkv, ob, ffg, g3, mods if modulated else None
+
+
+@pytest.mark.parametrize("modulated", [True, False])
+def test_block_forward_equals_the_public_calls(ctx, modulated):
+    """The block driver's fusions (the norm writing the fp16 copy q, k, v and
+    w1, w3 read; post-norm + residual in one pass) give the same bits as the
+    public entry points called one by one."""
+    import torch
+    rows = 136
+    ob, gp, desc = build_block(ctx, 900 + modulated, H, F, ADA, 4, modulated)
+    x = bf16(randn(47, (rows, H)))
+    temb = bf16(randn(49, (ADA,))) if modulated else None
+    c, s = tables(rows)
+    got = run_gpu(ctx, desc, dims(), x, rows, c, s, temb, SCALES)
+    xd, nrm, qkv, obd, ffg, g3, mods = public_block(ctx, gp, x, rows, c, s, temb, SCALES,
+                                                    modulated)
+    # the feed-forward half, public calls
+    y = torch.empty((rows, H), dtype=torch.int16, device="cuda")
+    ctx.ffn(gp["w1"], gp["w3"], gp["w2"], nrm, y, rows, SCALES, h=ffg)
+    ctx.rmsnorm(y, gp["fn2"], y, rows, H)
+    if modulated:
+        ctx.gated_residual(xd, mods[:, 3 * H:], y, rows, H)
+    else:
+        ctx.residual_add(xd, y, rows, H)
+    ctx.synchronize()
+    want = from_dev(xd)
+    assert np.array_equal(got, want)

@@ -104,6 +104,12 @@ hipError_t launch_repack(int bits, const uint32_t* codes,
 hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
                           uint16_t* y, long long ldy, int rows, int D,
                           float eps, hipStream_t s);
+// mode 0 plain; 1 also h = fp16(y); 2 h = bf16(h + tanh(gate) * y), y unused;
+// 3 h = bf16(h + y) (see rmsnorm_kernel)
+hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const uint16_t* w,
+                             uint16_t* y, long long ldy, uint16_t* h, long long ldh,
+                             const uint16_t* gate, int rows, int D, float eps,
+                             hipStream_t s);
 hipError_t launch_rope_table(const int32_t* pt, const int32_t* ph,
                              const int32_t* pw, int n, int a0, int a1, int a2,
                              int head_dim, double theta, float* cos_t,

@@ -110,31 +110,25 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
     g3 = w.nw3;
   }
   // ---- attention half ----
-  RC(ming_rmsnorm(c, x, H, g1, w.nrm, H, rows, H, eps));
-  RC(ming_lin(c, b->q, w.nrm, H, w.qkv, 3 * H, rows, scales));
-  RC(ming_lin(c, b->k, w.nrm, H, w.qkv + H, 3 * H, rows, scales));
-  RC(ming_lin(c, b->v, w.nrm, H, w.qkv + 2 * H, 3 * H, rows, scales));
+  // the norm also writes the fp16 copy q, k and v read (one conversion, not three)
+  RC(ming::rt_rmsnorm_f16(c, x, H, g1, w.nrm, H, rows, H, eps));
+  RC(ming::rt_lin_xh(c, b->q, w.nrm, H, w.qkv, 3 * H, rows, scales));
+  RC(ming::rt_lin_xh(c, b->k, w.nrm, H, w.qkv + H, 3 * H, rows, scales));
+  RC(ming::rt_lin_xh(c, b->v, w.nrm, H, w.qkv + 2 * H, 3 * H, rows, scales));
   RC(ming_qk_norm_rope(c, w.qkv, 3 * H, 0, H, rows, NH, 128, b->nq, b->nk, cos_t, sin_t,
                        eps));
   // the attention output reuses the normed-input plane (its q/k/v are done)
   RC(ming_attention(c, w.qkv, 3 * H, 0, H, 2 * H, w.nrm, H, rows, NH, 128,
                     1.0f / std::sqrt(128.0f)));
   RC(ming_lin(c, b->o, w.nrm, H, w.ob, H, rows, scales));
-  RC(ming_rmsnorm(c, w.ob, H, b->an2, w.ob, H, rows, H, eps));
-  if (modulated) {
-    RC(ming_gated_residual(c, x, H, w.mods + H, w.ob, H, rows, H));
-  } else {
-    RC(ming_residual_add(c, x, H, w.ob, H, rows, H));
-  }
+  // post-norm and the (gated) residual in one pass
+  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->an2, modulated ? w.mods + H : nullptr, rows,
+                            H, eps));
   // ---- feed-forward half (gpu_ff, 2151-2162; SwiGLU fused into w3) ----
-  RC(ming_rmsnorm(c, x, H, g3, w.nrm, H, rows, H, eps));
-  RC(ming_ffn(c, b->w1, b->w3, b->w2, w.nrm, H, w.ob, H, rows, scales, w.ffg, F));
-  RC(ming_rmsnorm(c, w.ob, H, b->fn2, w.ob, H, rows, H, eps));
-  if (modulated) {
-    RC(ming_gated_residual(c, x, H, w.mods + 3 * H, w.ob, H, rows, H));
-  } else {
-    RC(ming_residual_add(c, x, H, w.ob, H, rows, H));
-  }
+  RC(ming::rt_rmsnorm_f16(c, x, H, g3, w.nrm, H, rows, H, eps));
+  RC(ming::rt_ffn_xh(c, b->w1, b->w3, b->w2, w.nrm, H, w.ob, H, rows, scales, w.ffg, F));
+  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->fn2, modulated ? w.mods + 3 * H : nullptr,
+                            rows, H, eps));
   return MING_OK;
 }
 

@@ -19,11 +19,23 @@
 namespace ming {
 namespace {
 
-template <int LPR, int CPL>
+// MODE 0: y = rms(x) * w.
+// MODE 1: the same, plus h = fp16(y) (row stride ldh): the fp16 copy the fast
+//         projections read, so the projections after the norm skip their own
+//         bf16 -> fp16 pass (same bits: fp16 holds every bf16 value in range
+//         exactly, converted as bf16_to_f16 converts).
+// MODE 2: h = bf16(h + tanh(gate[n]) * y), y not stored: the post-norm and the
+//         gated residual of run_block (ming-dit.cc:2096-2100, 2256-2260) in one
+//         pass over the sub-layer output and the stream.
+// MODE 3: h = bf16(h + y): the same for the context refiner's plain residual.
+// Every mode reduces a row exactly as MODE 0 does and rounds y to bf16 before
+// the residual, so each is bit-identical to rmsnorm followed by the separate
+// residual / conversion kernel.
+template <int LPR, int CPL, int MODE>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(
     const uint16_t* x, long long ldx, const uint16_t* __restrict__ w,
-    uint16_t* y, long long ldy,
-    int rows, int D, float eps) {
+    uint16_t* y, long long ldy, uint16_t* h, long long ldh,
+    const uint16_t* __restrict__ gate, int rows, int D, float eps) {
   constexpr int RPW = 64 / LPR;  // rows per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
@@ -51,7 +63,15 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
   const float inv = 1.0f / sqrtf(ss / (float)D + eps);
   if (!live) return;
-  uint16_t* yr = y + (long long)row * ldy;
+  uint4 hv[CPL];
+  if (MODE >= 2) {  // the residual stream, loaded before any store of this row
+    const uint16_t* hr = h + (long long)row * ldh;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + LPR * i;
+      if (c < nch) hv[i] = *reinterpret_cast<const uint4*>(hr + 8 * c);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = sub + LPR * i;
@@ -67,7 +87,34 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
         const float b = __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv), bf16_hi(wu[e]));
         ou[e] = pack_bf16x2(a, b);
       }
-      *reinterpret_cast<uint4*>(yr + 8 * c) = o;
+      if (MODE <= 1) {
+        *reinterpret_cast<uint4*>(y + (long long)row * ldy + 8 * c) = o;
+        if (MODE == 1) {
+          uint4 f;
+          f.x = bf16x2_to_f16x2(o.x);
+          f.y = bf16x2_to_f16x2(o.y);
+          f.z = bf16x2_to_f16x2(o.z);
+          f.w = bf16x2_to_f16x2(o.w);
+          *reinterpret_cast<uint4*>(h + (long long)row * ldh + 8 * c) = f;
+        }
+      } else {
+        uint4 gv = make_uint4(0, 0, 0, 0);
+        if (MODE == 2) gv = *reinterpret_cast<const uint4*>(gate + 8 * c);
+        const uint32_t* hp = &hv[i].x;
+        const uint32_t* gp = &gv.x;
+        uint4 r;
+        uint32_t* rp = &r.x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float s0 = bf16_lo(ou[e]), s1 = bf16_hi(ou[e]);
+          if (MODE == 2) {
+            s0 = __fmul_rn(tanhf(bf16_lo(gp[e])), s0);
+            s1 = __fmul_rn(tanhf(bf16_hi(gp[e])), s1);
+          }
+          rp[e] = pack_bf16x2(__fadd_rn(bf16_lo(hp[e]), s0), __fadd_rn(bf16_hi(hp[e]), s1));
+        }
+        *reinterpret_cast<uint4*>(h + (long long)row * ldh + 8 * c) = r;
+      }
     }
   }
 }
@@ -155,17 +202,23 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 
 }  // namespace
 
-hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
-                          uint16_t* y, long long ldy, int rows, int D,
-                          float eps, hipStream_t s) {
+hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const uint16_t* w,
+                             uint16_t* y, long long ldy, uint16_t* h, long long ldh,
+                             const uint16_t* gate, int rows, int D, float eps,
+                             hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   const int nch = D / 8;
-  if (D % 8 != 0 || nch > 64 * 16) return hipErrorInvalidValue;
-#define MING_RMS(LPR, CPL)                                                   \
-  do {                                                                       \
-    const int rpb = 4 * (64 / (LPR));                                        \
-    hipLaunchKernelGGL((rmsnorm_kernel<LPR, CPL>), dim3((rows + rpb - 1) / rpb), \
-                       dim3(256), 0, s, x, ldx, w, y, ldy, rows, D, eps);    \
+  if (D % 8 != 0 || nch > 64 * 16 || mode < 0 || mode > 3) return hipErrorInvalidValue;
+#define MING_RMS_M(LPR, CPL, MODE)                                                \
+  hipLaunchKernelGGL((rmsnorm_kernel<LPR, CPL, MODE>), dim3((rows + rpb - 1) / rpb), \
+                     dim3(256), 0, s, x, ldx, w, y, ldy, h, ldh, gate, rows, D, eps)
+#define MING_RMS(LPR, CPL)                                                     \
+  do {                                                                         \
+    const int rpb = 4 * (64 / (LPR));                                          \
+    if (mode == 0) MING_RMS_M(LPR, CPL, 0);                                    \
+    else if (mode == 1) MING_RMS_M(LPR, CPL, 1);                               \
+    else if (mode == 2) MING_RMS_M(LPR, CPL, 2);                               \
+    else MING_RMS_M(LPR, CPL, 3);                                              \
   } while (0)
   if (nch <= 8) MING_RMS(8, 1);
   else if (nch <= 16) MING_RMS(16, 1);
@@ -175,7 +228,14 @@ hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
   else if (nch <= 512) MING_RMS(64, 8);
   else MING_RMS(64, 16);
 #undef MING_RMS
+#undef MING_RMS_M
   return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
+                          uint16_t* y, long long ldy, int rows, int D,
+                          float eps, hipStream_t s) {
+  return launch_rmsnorm_ex(0, x, ldx, w, y, ldy, nullptr, 0, nullptr, rows, D, eps, s);
 }
 
 hipError_t launch_rope_table(const int32_t* pt, const int32_t* ph,
@@ -210,13 +270,14 @@ namespace ming {
 hipError_t validate_norm_kernels() {
   hipFuncAttributes fa;
   const void* fns[] = {
-      reinterpret_cast<const void*>(&rmsnorm_kernel<8, 1>),
-      reinterpret_cast<const void*>(&rmsnorm_kernel<16, 1>),
-      reinterpret_cast<const void*>(&rmsnorm_kernel<32, 1>),
-      reinterpret_cast<const void*>(&rmsnorm_kernel<64, 1>),
-      reinterpret_cast<const void*>(&rmsnorm_kernel<64, 4>),
-      reinterpret_cast<const void*>(&rmsnorm_kernel<64, 8>),
-      reinterpret_cast<const void*>(&rmsnorm_kernel<64, 16>),
+#define MING_RMS_ALL(LPR, CPL)                                      \
+  reinterpret_cast<const void*>(&rmsnorm_kernel<LPR, CPL, 0>),      \
+      reinterpret_cast<const void*>(&rmsnorm_kernel<LPR, CPL, 1>),  \
+      reinterpret_cast<const void*>(&rmsnorm_kernel<LPR, CPL, 2>),  \
+      reinterpret_cast<const void*>(&rmsnorm_kernel<LPR, CPL, 3>)
+      MING_RMS_ALL(8, 1),  MING_RMS_ALL(16, 1), MING_RMS_ALL(32, 1), MING_RMS_ALL(64, 1),
+      MING_RMS_ALL(64, 4), MING_RMS_ALL(64, 8), MING_RMS_ALL(64, 16),
+#undef MING_RMS_ALL
       reinterpret_cast<const void*>(&rope_table_kernel),
       reinterpret_cast<const void*>(&qk_norm_rope_kernel)};
   for (const void* f : fns) {

@@ -579,7 +579,23 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fk = lane >> 5;
   const int wm = wave & 1, wc = wave >> 1;
-  const int m0 = blockIdx.x * 256, c0 = blockIdx.y * 128, ks = blockIdx.z;
+  // XCD-aware order: block b runs on XCD b % 8, so each XCD takes a
+  // contiguous run of work items, ordered (slice, row block, column block)
+  // with the column blocks fastest. The blocks that read the same x rows
+  // then run side by side on one XCD and share its L2 instead of each
+  // fetching x from HBM.
+  int m0, c0, ks;
+  {
+    const int tiles_m = (a.M + 255) / 256, tiles_c = (a.n_cols + 127) / 128;
+    const int nb = (int)gridDim.x;
+    const int q = nb / 8, rem = nb % 8;
+    const int xcd = (int)blockIdx.x % 8, local = (int)blockIdx.x / 8;
+    const int v = xcd * q + (xcd < rem ? xcd : rem) + local;
+    const int tc = v % tiles_c, rest = v / tiles_c;
+    m0 = (rest % tiles_m) * 256;
+    c0 = tc * 128;
+    ks = rest / tiles_m;
+  }
   const int KT = a.K / 64;
   const int kt0 = (int)((long long)KT * ks / kslices);
   const int kt1 = (int)((long long)KT * (ks + 1) / kslices);
@@ -857,8 +873,8 @@ int lora_xa_fast_slices(int M, int n_cols, int K) {
 hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s) {
   if (a.M <= 0 || a.n_cols <= 0) return hipSuccess;
-  dim3 grid((a.M + 255) / 256, (a.n_cols + 127) / 128, kslices);
-  hipLaunchKernelGGL(lora_xa_fast_kernel, grid, dim3(256), 0, s, a, part, kslices);
+  const unsigned nblk = (unsigned)(((a.M + 255) / 256) * ((a.n_cols + 127) / 128) * kslices);
+  hipLaunchKernelGGL(lora_xa_fast_kernel, dim3(nblk), dim3(256), 0, s, a, part, kslices);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || kslices == 1) return e;
   long long work = (long long)a.M * (a.n_cols / 4);

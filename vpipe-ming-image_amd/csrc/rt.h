@@ -5,6 +5,7 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
 #include <string>
 
 #include "../../include/ming_dit_amd.h"
@@ -22,4 +23,23 @@ void rt_log(int level, const std::string& msg);
 int rt_upload(ming_ctx* c, const void* host, size_t bytes, void** dev);
 void rt_free(ming_ctx* c, void* dev);
 void rt_note_cap_hit(ming_ctx* c);
+
+// Fused forms the block driver uses (same bits as the public calls they
+// replace):
+// y = rmsnorm(x) and the context's fp16 copy of y, which the next projections
+// over y then read instead of converting y themselves (rt_lin_xh, rt_ffn_xh
+// are only valid while that copy still holds y: no other projection between);
+int rt_rmsnorm_f16(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                   uint16_t* y, int64_t ldy, int rows, int D, float eps);
+int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ldx,
+              uint16_t* y, int64_t ldy, int M, const float* scales);
+int rt_ffn_xh(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
+              const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
+              int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh);
+// h = bf16(h + tanh(gate) * rmsnorm(sub)) (gate NULL: h + rmsnorm(sub)), sub
+// left as it was: ming_rmsnorm in place followed by ming_gated_residual /
+// ming_residual_add.
+int rt_norm_residual(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
+                     int64_t lds, const uint16_t* w, const uint16_t* gate, int rows, int D,
+                     float eps);
 }  // namespace ming

@@ -92,13 +92,13 @@ namespace {
 // marks, ming-dit.cc:1689-1717, as HIP events around each launch).
 enum Bucket {
   kBQ4, kBQ8, kBDense, kBF4, kBF8, kBCvt, kBXa, kBRms, kBQkRope, kBRopeTab, kBSwiglu, kBResid,
-  kBModulate, kBBias, kBLn, kBQuant, kBAttn, kBCount
+  kBModulate, kBBias, kBLn, kBQuant, kBAttn, kBNormRes, kBCount
 };
 const char* const kBucketName[kBCount] = {
     "qproj.w4", "qproj.w8", "qproj.dense", "qproj_fast.w4", "qproj_fast.w8",
     "cvt_f16", "lora_xa", "rmsnorm",
     "qk_norm_rope", "rope_table", "swiglu", "residual", "modulate",
-    "bias_act", "ln_modulate", "quantize", "attention"};
+    "bias_act", "ln_modulate", "quantize", "attention", "norm_residual"};
 
 hipEvent_t take_event(ming_ctx* c) {
   if (!c->pool.empty()) {
@@ -918,9 +918,11 @@ int ming_lin_swiglu(ming_ctx* c, const ming_qweight* w, const uint16_t* x,
   return lin_impl(c, w, x, ldx, out, ldo, M, scales, g, ldg, false, nullptr);
 }
 
-int ming_ffn(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
-             const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
-             int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh) {
+// gpu_ff; xh_ready: the context's fp16 copy already holds x (row stride H).
+static int ffn_impl(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
+                    const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
+                    int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh,
+                    bool xh_ready) {
   if (!c || !w1 || !w3 || !w2 || !x || !y || !h)
     return fail(MING_ERR_ARG, "ming_ffn: null argument");
   const int F = w1->N, H = w1->K;
@@ -929,31 +931,59 @@ int ming_ffn(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
   if (ldh < F || ldh % 8 != 0 || !aligned(h, 16))
     return fail(MING_ERR_SHAPE, "ming_ffn: h needs ldh >= ffn, ldh % 8 == 0, 16-byte alignment");
   bool fast1 = false;
-  int rc = lin_impl(c, w1, x, ldx, h, ldh, M, scales, nullptr, 0, false, &fast1);
+  int rc = lin_impl(c, w1, x, ldx, h, ldh, M, scales, nullptr, 0, xh_ready, &fast1);
   if (rc != MING_OK) return rc;
   // w3 reads the same x: the fp16 copy w1's fast route made serves it too
-  rc = lin_impl(c, w3, x, ldx, h, ldh, M, scales, h, ldh, fast1, nullptr);
+  rc = lin_impl(c, w3, x, ldx, h, ldh, M, scales, h, ldh, xh_ready || fast1, nullptr);
   if (rc != MING_OK) return rc;
   return lin_impl(c, w2, h, ldh, y, ldy, M, scales, nullptr, 0, false, nullptr);
 }
 
-int ming_rmsnorm(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* w,
-                 uint16_t* y, int64_t ldy, int rows, int D, float eps) {
-  if (!c || !x || !w || !y) return fail(MING_ERR_ARG, "ming_rmsnorm: null argument");
+int ming_ffn(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
+             const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
+             int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh) {
+  return ffn_impl(c, w1, w3, w2, x, ldx, y, ldy, M, scales, h, ldh, false);
+}
+
+// The RMSNorm kernel's modes (see rmsnorm_kernel): 0 plain; 1 also the
+// context's fp16 copy of y; 2 / 3 post-norm fused into the gated / plain
+// residual h += (tanh(gate) *) y.
+static int rms_impl(ming_ctx* c, int mode, const uint16_t* x, int64_t ldx,
+                    const uint16_t* w, uint16_t* y, int64_t ldy, uint16_t* h,
+                    int64_t ldh, const uint16_t* gate, int rows, int D, float eps,
+                    const char* who) {
+  if (!c || !x || !w || (mode <= 1 && !y) || (mode >= 2 && !h) || (mode == 2 && !gate))
+    return fail(MING_ERR_ARG, std::string(who) + ": null argument");
   if (rows < 0 || D <= 0 || D % 8 != 0 || D > 8192)
-    return fail(MING_ERR_SHAPE, "ming_rmsnorm: need D % 8 == 0 and D <= 8192");
-  if (ldx < D || ldy < D || ldx % 8 != 0 || ldy % 8 != 0)
-    return fail(MING_ERR_SHAPE, "ming_rmsnorm: bad row strides");
-  if (!aligned(x, 16) || !aligned(y, 16) || !aligned(w, 16))
-    return fail(MING_ERR_ARG, "ming_rmsnorm: pointers must be 16-byte aligned");
+    return fail(MING_ERR_SHAPE, std::string(who) + ": need D % 8 == 0 and D <= 8192");
+  if (ldx < D || ldx % 8 != 0 || (mode <= 1 && (ldy < D || ldy % 8 != 0)) ||
+      (mode >= 2 && (ldh < D || ldh % 8 != 0)))
+    return fail(MING_ERR_SHAPE, std::string(who) + ": bad row strides");
+  if (!aligned(x, 16) || !aligned(w, 16) || (mode <= 1 && !aligned(y, 16)) ||
+      (mode >= 2 && !aligned(h, 16)) || (mode == 2 && !aligned(gate, 16)))
+    return fail(MING_ERR_ARG, std::string(who) + ": pointers must be 16-byte aligned");
   if (rows == 0) return ok();
   DeviceGuard g(c->device);
-  MING_HIP(profiled(c, kBRms, 0.0, 4.0 * rows * D + 2.0 * D,
-                    [&] { return ming::launch_rmsnorm(x, ldx, w, y, ldy, rows, D,
-                                                      eps, c->stream); }),
+  if (mode == 1) {
+    int rc = ensure_xh(c, (size_t)rows * D * 2);
+    if (rc != MING_OK) return rc;
+    h = (uint16_t*)c->xh;
+    ldh = D;
+  }
+  const double bytes = (mode == 0 ? 4.0 : 6.0) * rows * D + (mode == 2 ? 4.0 : 2.0) * D;
+  MING_HIP(profiled(c, mode >= 2 ? kBNormRes : kBRms, 0.0, bytes,
+                    [&] { return ming::launch_rmsnorm_ex(mode, x, ldx, w, y, ldy, h, ldh,
+                                                         gate, rows, D, eps, c->stream); }),
            "rmsnorm launch");
   c->eng.rmsnorm += 1;
+  if (mode >= 2) c->eng.elementwise += 1;
   return ok();
+}
+
+int ming_rmsnorm(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                 uint16_t* y, int64_t ldy, int rows, int D, float eps) {
+  return rms_impl(c, 0, x, ldx, w, y, ldy, nullptr, 0, nullptr, rows, D, eps,
+                  "ming_rmsnorm");
 }
 
 int ming_rope_table(ming_ctx* c, const int32_t* pos_t, const int32_t* pos_h,
@@ -1267,4 +1297,27 @@ void rt_free(ming_ctx* c, void* dev) {
 }
 
 void rt_note_cap_hit(ming_ctx* c) { c->eng.cap_cache_hits += 1; }
+
+int rt_rmsnorm_f16(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                   uint16_t* y, int64_t ldy, int rows, int D, float eps) {
+  return rms_impl(c, 1, x, ldx, w, y, ldy, nullptr, 0, nullptr, rows, D, eps, "rmsnorm");
+}
+
+int rt_norm_residual(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
+                     int64_t lds, const uint16_t* w, const uint16_t* gate, int rows, int D,
+                     float eps) {
+  return rms_impl(c, gate ? 2 : 3, sub, lds, w, nullptr, 0, h, ldh, gate, rows, D, eps,
+                  "post-norm residual");
+}
+
+int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ldx,
+              uint16_t* y, int64_t ldy, int M, const float* scales) {
+  return lin_impl(c, qw, x, ldx, y, ldy, M, scales, nullptr, 0, true, nullptr);
+}
+
+int rt_ffn_xh(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
+              const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
+              int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh) {
+  return ffn_impl(c, w1, w3, w2, x, ldx, y, ldy, M, scales, h, ldh, true);
+}
 }  // namespace ming
