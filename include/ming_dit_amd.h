@@ -460,6 +460,45 @@ int ming_model_lora_modules(const ming_model* m, int slot);
 int ming_model_lora_skipped(const ming_model* m, int slot);
 const char* ming_model_lora_report(const ming_model* m, int slot);
 
+/* ---- the denoise loop (MingImageGenerator::generate, ming-generator.cc:352-577) -----
+ * schedule_sigmas (ming-generator.cc:158-174): out[k] = f32(shift*u / (1 + (shift-1)*u)),
+ * u = 1 - k/steps, k < steps, computed in double; out[steps] = 0. `out` holds steps+1. */
+int ming_schedule_sigmas(int steps, float shift, float* out);
+
+typedef struct ming_denoise_args {
+  /* the positive caption (device bf16 [cap_len][cap_stride]) and its layout's
+   * positions (host int32 [img_tokens + cap_len] per axis, image rows first) */
+  const uint16_t* cap;
+  int64_t cap_stride;
+  int cap_len, query_rows;
+  const int32_t *pos_t, *pos_h, *pos_w;
+  /* the negative for classifier-free guidance: NULL is the reference's default,
+   * the positive's shape times zero (then its layout is the positive's);
+   * otherwise neg_len rows of the same stride and their own positions */
+  const uint16_t* cap_neg;
+  int neg_len, neg_query_rows;
+  const int32_t *neg_pos_t, *neg_pos_h, *neg_pos_w;
+  int img_tokens;
+  int steps;                 /* forwards (11 by default in the reference) */
+  float shift;               /* the checkpoint's static shift (6.0) */
+  float guidance;            /* > 1 runs the negative and guides */
+  double cfg_truncation;     /* guide while (1 - sigma) <= this (1.0: always) */
+  double cfg_normalization;  /* > 0: clamp |guided| to this x |positive| */
+} ming_denoise_args;
+
+/* progress(user, step, steps) after each step; returning 0 stops the loop. */
+typedef int (*ming_step_fn)(void* user, int step, int steps);
+
+/* The flow-match Euler loop over the model, with the reference's host
+ * arithmetic in f32: per step the latent is rounded to bf16 (NaN -> 0x7fc0),
+ * v = forward(positive); when guided, v = p + g*(p - forward(negative)) with
+ * the optional norm clamp; then latents += (sigma[i+1] - sigma[i]) * -v.
+ * latents: host f32 [img_tokens][patch_dim], the packed noise in, the
+ * denoised latent out. Returns MING_STOPPED when the model's stop callback or
+ * `progress` stopped it (latents then hold the last completed step). */
+int ming_model_denoise(ming_model* m, const ming_denoise_args* a, float* latents,
+                       ming_step_fn progress, void* user);
+
 #ifdef __cplusplus
 }
 #endif

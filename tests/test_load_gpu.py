@@ -343,3 +343,75 @@ def test_load_refuses_what_it_does_not_run(ctx, tmp_path):
     make_checkpoint(d, seed=12, cfg=CFG, shards=1, drop=("layers.1.ffn_norm2.weight",))
     with pytest.raises(m.MingError, match="layers.1.ffn_norm2.weight' is not in the checkpoint"):
         m.Model.load(ctx, d)
+
+
+def reference_loop(ctx, model, lat0, cap, lay, steps, shift, g, trunc=1.0,
+                   stop_after=None):
+    """The generator's loop (ming-generator.cc:505-577) restated in numpy
+    f32 over the same model's forwards: bf16 latent per step (NaN -> 0x7fc0),
+    v = pos (+ g (pos - neg) while (1 - sigma) <= trunc, negative = the
+    caption times zero), latent += (sigma[i+1] - sigma[i]) * -v."""
+    lay_, img, _, cap_h, cs = lay
+    sig = np.asarray(orc.schedule_sigmas(steps, shift), np.float32)
+    x = lat0.copy()
+    zero = np.zeros_like(cap_h)
+    for i in range(steps if stop_after is None else stop_after):
+        inp = (lay_, img, orc.f32_to_bf16(x), cap_h, cs)
+        v = f32(run(model, inp, float(sig[i])))
+        if g > 1.0 and (1.0 - float(sig[i])) <= trunc:
+            vn = f32(run(model, (lay_, img, orc.f32_to_bf16(x), zero, cs), float(sig[i])))
+            v = (v + np.float32(g) * (v - vn)).astype(np.float32)
+        dt = np.float32(sig[i + 1] - sig[i])
+        x = (x + dt * -v).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("g,trunc", [(1.0, 1.0), (4.0, 1.0), (3.0, 0.2)])
+def test_denoise_loop_equals_its_restatement(ctx, files, g, trunc):
+    model = m.Model.load(ctx, files["w4"], [(files["ad"]["diffusers"], 0.7)])
+    lay, img, lat, cap, cs = inputs()
+    lat0 = randn(71, (img, PD))
+    steps = 3
+    want = reference_loop(ctx, model, lat0, None, (lay, img, None, cap, cs), steps, 6.0, g,
+                          trunc)
+    x = lat0.copy()
+    cd = to_dev(cap)
+    model.set_caption_cache(False)     # cold: the restatement's forwards filled it
+    model.set_caption_cache(True)
+    ctx.reset_engagement()
+    assert model.denoise(x, cd, cs, CAP, QROWS, (lay["pos_t"], lay["pos_h"], lay["pos_w"]),
+                         img, steps, 6.0, g, trunc)
+    assert np.array_equal(x, want)
+    # the caption cache serves the context refiner after the first step, for
+    # the positive and (while guided) the zero negative
+    sig = orc.schedule_sigmas(steps, 6.0)
+    guided = [g > 1.0 and (1.0 - float(s)) <= trunc for s in sig[:steps]]
+    assert ctx.engagement()["cap_cache_hits"] == (steps - 1) + max(sum(guided) - 1, 0)
+    model.close()
+
+
+def test_denoise_stops_and_clamps(ctx, files):
+    model = m.Model.load(ctx, files["w4"])
+    lay, img, lat, cap, cs = inputs()
+    lat0 = randn(73, (img, PD))
+    pos = (lay["pos_t"], lay["pos_h"], lay["pos_w"])
+    cd = to_dev(cap)
+    seen = []
+    x = lat0.copy()
+    assert not model.denoise(x, cd, cs, CAP, QROWS, pos, img, 4, 6.0, 4.0,
+                             progress=lambda i, n: seen.append((i, n)) or i < 2)
+    assert seen == [(1, 4), (2, 4)]
+    want = reference_loop(ctx, model, lat0, None, (lay, img, None, cap, cs), 4, 6.0, 4.0,
+                          stop_after=2)
+    assert np.array_equal(x, want)
+    # the norm clamp: |guided| <= cfg_normalization x |positive| on the one step
+    sig = orc.schedule_sigmas(1, 6.0)
+    x1, x2 = lat0.copy(), lat0.copy()
+    assert model.denoise(x1, cd, cs, CAP, QROWS, pos, img, 1, 6.0, 4.0)
+    assert model.denoise(x2, cd, cs, CAP, QROWS, pos, img, 1, 6.0, 4.0, cfg_normalization=1.0)
+    v_free = (x1 - lat0) / np.float32(sig[0])      # the guided velocity
+    v_clamp = (x2 - lat0) / np.float32(sig[0])
+    vp = f32(run(model, (lay, img, orc.f32_to_bf16(lat0), cap, cs), float(sig[0])))
+    assert np.linalg.norm(v_free) > 1.05 * np.linalg.norm(vp)
+    assert abs(np.linalg.norm(v_clamp) / np.linalg.norm(vp) - 1.0) < 1e-3
+    model.close()

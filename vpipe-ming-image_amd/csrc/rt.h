@@ -22,6 +22,10 @@ void rt_log(int level, const std::string& msg);
 // a device copy of `bytes` host bytes on the context's device (NULL for 0)
 int rt_upload(ming_ctx* c, const void* host, size_t bytes, void** dev);
 void rt_free(ming_ctx* c, void* dev);
+int rt_alloc(ming_ctx* c, size_t bytes, bool zero, void** dev);
+// ordered on the context's stream, and waited for
+int rt_h2d(ming_ctx* c, void* dev, const void* host, size_t bytes);
+int rt_d2h(ming_ctx* c, void* host, const void* dev, size_t bytes);
 void rt_note_cap_hit(ming_ctx* c);
 
 // Fused forms the block driver uses (same bits as the public calls they

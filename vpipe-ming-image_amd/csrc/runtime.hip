@@ -1290,6 +1290,39 @@ int rt_upload(ming_ctx* c, const void* host, size_t bytes, void** dev) {
   return ok();
 }
 
+int rt_alloc(ming_ctx* c, size_t bytes, bool zero, void** dev) {
+  *dev = nullptr;
+  DeviceGuard dg(c->device);
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MING_ERR_ALLOC, "device allocation of " + std::to_string(bytes) + " bytes failed");
+  }
+  if (zero && (hipMemsetAsync(p, 0, bytes, c->stream) != hipSuccess ||
+               hipStreamSynchronize(c->stream) != hipSuccess)) {
+    (void)hipFree(p);
+    return fail(MING_ERR_HIP, "device memset failed");
+  }
+  *dev = p;
+  return ok();
+}
+
+int rt_h2d(ming_ctx* c, void* dev, const void* host, size_t bytes) {
+  DeviceGuard dg(c->device);
+  if (hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
+    return fail(MING_ERR_HIP, "host to device copy failed");
+  return ok();
+}
+
+int rt_d2h(ming_ctx* c, void* host, const void* dev, size_t bytes) {
+  DeviceGuard dg(c->device);
+  if (hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
+    return fail(MING_ERR_HIP, "device to host copy failed");
+  return ok();
+}
+
 void rt_free(ming_ctx* c, void* dev) {
   if (!dev) return;
   DeviceGuard dg(c->device);

@@ -100,7 +100,23 @@ class LoraSpec(C.Structure):
     _fields_ = [("path", C.c_char_p), ("scale", C.c_float)]
 
 
+class DenoiseArgs(C.Structure):
+    _fields_ = [("cap", C.c_void_p), ("cap_stride", C.c_int64),
+                ("cap_len", C.c_int), ("query_rows", C.c_int),
+                ("pos_t", C.POINTER(C.c_int32)), ("pos_h", C.POINTER(C.c_int32)),
+                ("pos_w", C.POINTER(C.c_int32)),
+                ("cap_neg", C.c_void_p), ("neg_len", C.c_int),
+                ("neg_query_rows", C.c_int),
+                ("neg_pos_t", C.POINTER(C.c_int32)),
+                ("neg_pos_h", C.POINTER(C.c_int32)),
+                ("neg_pos_w", C.POINTER(C.c_int32)),
+                ("img_tokens", C.c_int), ("steps", C.c_int), ("shift", C.c_float),
+                ("guidance", C.c_float), ("cfg_truncation", C.c_double),
+                ("cfg_normalization", C.c_double)]
+
+
 LOG_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_char_p)
+STEP_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int)
 STOP_FN = C.CFUNCTYPE(C.c_int, C.c_void_p)
 PROGRESS_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_int)
 STOPPED = -1
@@ -197,6 +213,9 @@ def lib():
         "ming_model_lora_modules": ([vp, i32], i32),
         "ming_model_lora_skipped": ([vp, i32], i32),
         "ming_model_lora_report": ([vp, i32], C.c_char_p),
+        "ming_schedule_sigmas": ([i32, f32, C.POINTER(f32)], i32),
+        "ming_model_denoise": ([vp, C.POINTER(DenoiseArgs), C.POINTER(f32), STEP_FN,
+                                vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -489,6 +508,14 @@ def block_desc(**parts) -> BlockDesc:
 _log_keep = None
 
 
+def schedule_sigmas(steps: int, shift: float):
+    import numpy as np
+    out = np.zeros(steps + 1, np.float32)
+    _check(lib().ming_schedule_sigmas(int(steps), float(shift),
+                                      out.ctypes.data_as(C.POINTER(C.c_float))))
+    return out
+
+
 def set_log_sink(fn=None):
     """Route the library's session log to fn(level, message) (None: drop)."""
     global _log_keep
@@ -644,6 +671,39 @@ class Model:
 
     def set_caption_cache(self, on: bool):
         _check(lib().ming_model_set_caption_cache(self.h, int(bool(on))))
+
+    def denoise(self, latents, cap, cap_stride: int, cap_len: int,
+                query_rows: int, pos, img_tokens: int, steps: int,
+                shift: float = 6.0, guidance: float = 1.0,
+                cfg_truncation: float = 1.0, cfg_normalization: float = 0.0,
+                cap_neg=None, neg_len: int = 0, neg_query_rows: int = 0,
+                neg_pos=None, progress=None) -> bool:
+        """The generator's Euler loop; latents: host f32 [img][patch_dim],
+        updated in place. pos / neg_pos: (pos_t, pos_h, pos_w). True when
+        every step ran, False when stopped."""
+        import numpy as np
+        assert latents.dtype == np.float32 and latents.flags.c_contiguous
+        keep = [np.ascontiguousarray(p, np.int32) for p in pos]
+        a = DenoiseArgs()
+        a.cap, a.cap_stride, a.cap_len, a.query_rows = _ptr(cap), cap_stride, cap_len, query_rows
+        a.pos_t, a.pos_h, a.pos_w = [k.ctypes.data_as(C.POINTER(C.c_int32)) for k in keep]
+        if cap_neg is not None:
+            nk = [np.ascontiguousarray(p, np.int32) for p in neg_pos]
+            keep += nk
+            a.cap_neg, a.neg_len, a.neg_query_rows = _ptr(cap_neg), neg_len, neg_query_rows
+            a.neg_pos_t, a.neg_pos_h, a.neg_pos_w = [
+                k.ctypes.data_as(C.POINTER(C.c_int32)) for k in nk]
+        a.img_tokens, a.steps, a.shift, a.guidance = img_tokens, steps, shift, guidance
+        a.cfg_truncation, a.cfg_normalization = cfg_truncation, cfg_normalization
+        cb = (STEP_FN(lambda _u, i, n: 1 if progress(int(i), int(n)) else 0)
+              if progress else STEP_FN())
+        rc = lib().ming_model_denoise(self.h, C.byref(a),
+                                      latents.ctypes.data_as(C.POINTER(C.c_float)),
+                                      cb, None)
+        if rc == STOPPED:
+            return False
+        _check(rc)
+        return True
 
     def forward(self, latents, cap, cap_stride: int, img_tokens: int,
                 cap_len: int, query_rows: int, pos_t, pos_h, pos_w,
