@@ -43,6 +43,16 @@ __global__ void swiglu_kernel(const uint16_t* g, long long ldg,
   }
 }
 
+// t[i] = tanh(gate_msa[i]), t[n + i] = tanh(gate_mlp[i]) from the block's
+// adaLN output [scale_msa | gate_msa | scale_mlp | gate_mlp], with tanhf on
+// the bf16 value exactly as residual_kernel applies it per element.
+__global__ void tanh_gates_kernel(const uint16_t* mods, int n, float* t) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 2 * n) return;
+  const int src = i < n ? n + i : 3 * n + (i - n);
+  t[i] = tanhf(bf16_to_f32(mods[src]));
+}
+
 // mode 0: h += tanh(gate[n]) * sub ; mode 1: h += sub
 __global__ void residual_kernel(uint16_t* h, long long ldh, const uint16_t* gate,
                                 const uint16_t* sub, long long lds, int rows,
@@ -212,6 +222,12 @@ hipError_t launch_swiglu(const uint16_t* g, long long ldg, const uint16_t* u,
   return hipGetLastError();
 }
 
+hipError_t launch_tanh_gates(const uint16_t* mods, int n, float* t, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(tanh_gates_kernel, dim3((2 * n + 255) / 256), dim3(256), 0, s, mods, n, t);
+  return hipGetLastError();
+}
+
 hipError_t launch_residual(uint16_t* h, long long ldh, const uint16_t* gate,
                            const uint16_t* sub, long long lds, int rows, int n,
                            int gated, hipStream_t s) {
@@ -262,7 +278,8 @@ hipError_t validate_elementwise_kernels() {
                        reinterpret_cast<const void*>(&modulate_kernel),
                        reinterpret_cast<const void*>(&bias_act_kernel),
                        reinterpret_cast<const void*>(&ln_modulate_kernel),
-                       reinterpret_cast<const void*>(&quantize_kernel)};
+                       reinterpret_cast<const void*>(&quantize_kernel),
+                       reinterpret_cast<const void*>(&tanh_gates_kernel)};
   for (const void* f : fns) {
     const hipError_t e = hipFuncGetAttributes(&fa, f);
     if (e != hipSuccess) return e;

@@ -51,6 +51,10 @@ struct QprojArgs {
   // y = bf16(silu(g) * bf16(x . W^T + LoRA)) (g bf16 [M][ldg], may equal y)
   const uint16_t* g;
   long long ldg;
+  // optional fp16 copy of the (final) output, [M][ldyh], 16-byte aligned,
+  // ldyh % 8 == 0: the next projection's fast-route input (fast kernel only)
+  uint16_t* yh;
+  long long ldyh;
   QprojSeg seg[kMaxSeg];
   int16_t grp[kMaxGroups];
 };
@@ -104,12 +108,15 @@ hipError_t launch_repack(int bits, const uint32_t* codes,
 hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
                           uint16_t* y, long long ldy, int rows, int D,
                           float eps, hipStream_t s);
-// mode 0 plain; 1 also h = fp16(y); 2 h = bf16(h + tanh(gate) * y), y unused;
-// 3 h = bf16(h + y) (see rmsnorm_kernel)
+// mode 0 plain; 1 also h = fp16(y); 2 h = bf16(h + tg * y) with tg = tanh(gate)
+// in f32, y unused; 3 h = bf16(h + y) (see rmsnorm_kernel)
 hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const uint16_t* w,
                              uint16_t* y, long long ldy, uint16_t* h, long long ldh,
-                             const uint16_t* gate, int rows, int D, float eps,
+                             const float* tg, int rows, int D, float eps,
                              hipStream_t s);
+// t[i] = tanhf(bf16 g[i]) for the two gates of a block's adaLN output:
+// g = mods + n (gate_msa) and mods + 3n (gate_mlp) -> t[0, n) and t[n, 2n)
+hipError_t launch_tanh_gates(const uint16_t* mods, int n, float* t, hipStream_t s);
 hipError_t launch_rope_table(const int32_t* pt, const int32_t* ph,
                              const int32_t* pw, int n, int a0, int a1, int a2,
                              int head_dim, double theta, float* cos_t,

@@ -39,6 +39,7 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct BlockWs {
   uint16_t *nrm, *qkv, *ob, *ffg, *mods, *nw1, *nw3;
+  float* tg;  // tanh of the two residual gates, f32 [2H]
 };
 
 size_t block_ws_layout(const ming_block_dims& d, int rows, char* base, BlockWs* w) {
@@ -51,6 +52,8 @@ size_t block_ws_layout(const ming_block_dims& d, int rows, char* base, BlockWs* 
     if (base) *dst[i] = reinterpret_cast<uint16_t*>(base + off);
     off += align256(sz[i]);
   }
+  if (base) w->tg = reinterpret_cast<float*>(base + off);
+  off += align256(2 * H * 4);
   return off;
 }
 
@@ -106,6 +109,7 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
     RC(ming_bias_act(c, w.mods, 4 * H, b->ada_b, 1, 4 * H, 0));
     RC(ming_modulate(c, b->an1, H, w.mods, w.nw1, H, 1, H));
     RC(ming_modulate(c, b->fn1, H, w.mods + 2 * H, w.nw3, H, 1, H));
+    RC(ming::rt_tanh_gates(c, w.mods, H, w.tg));
     g1 = w.nw1;
     g3 = w.nw3;
   }
@@ -122,13 +126,13 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
                     1.0f / std::sqrt(128.0f)));
   RC(ming_lin(c, b->o, w.nrm, H, w.ob, H, rows, scales));
   // post-norm and the (gated) residual in one pass
-  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->an2, modulated ? w.mods + H : nullptr, rows,
-                            H, eps));
+  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->an2, modulated ? w.tg : nullptr, rows, H,
+                            eps));
   // ---- feed-forward half (gpu_ff, 2151-2162; SwiGLU fused into w3) ----
   RC(ming::rt_rmsnorm_f16(c, x, H, g3, w.nrm, H, rows, H, eps));
   RC(ming::rt_ffn_xh(c, b->w1, b->w3, b->w2, w.nrm, H, w.ob, H, rows, scales, w.ffg, F));
-  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->fn2, modulated ? w.mods + 3 * H : nullptr,
-                            rows, H, eps));
+  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->fn2, modulated ? w.tg + H : nullptr, rows,
+                            H, eps));
   return MING_OK;
 }
 

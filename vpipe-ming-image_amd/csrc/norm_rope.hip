@@ -24,9 +24,11 @@ namespace {
 //         projections read, so the projections after the norm skip their own
 //         bf16 -> fp16 pass (same bits: fp16 holds every bf16 value in range
 //         exactly, converted as bf16_to_f16 converts).
-// MODE 2: h = bf16(h + tanh(gate[n]) * y), y not stored: the post-norm and the
-//         gated residual of run_block (ming-dit.cc:2096-2100, 2256-2260) in one
-//         pass over the sub-layer output and the stream.
+// MODE 2: h = bf16(h + tg[n] * y), y not stored, tg = tanh(gate) in f32
+//         computed once per block (tanhf of the bf16 gate, as the residual
+//         kernel computes it per element): the post-norm and the gated residual
+//         of run_block (ming-dit.cc:2096-2100, 2256-2260) in one pass over the
+//         sub-layer output and the stream.
 // MODE 3: h = bf16(h + y): the same for the context refiner's plain residual.
 // Every mode reduces a row exactly as MODE 0 does and rounds y to bf16 before
 // the residual, so each is bit-identical to rmsnorm followed by the separate
@@ -35,7 +37,7 @@ template <int LPR, int CPL, int MODE>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(
     const uint16_t* x, long long ldx, const uint16_t* __restrict__ w,
     uint16_t* y, long long ldy, uint16_t* h, long long ldh,
-    const uint16_t* __restrict__ gate, int rows, int D, float eps) {
+    const float* __restrict__ tg, int rows, int D, float eps) {
   constexpr int RPW = 64 / LPR;  // rows per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
@@ -98,18 +100,22 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
           *reinterpret_cast<uint4*>(h + (long long)row * ldh + 8 * c) = f;
         }
       } else {
-        uint4 gv = make_uint4(0, 0, 0, 0);
-        if (MODE == 2) gv = *reinterpret_cast<const uint4*>(gate + 8 * c);
+        float t[8];
+        if (MODE == 2) {
+          const float4 t0 = *reinterpret_cast<const float4*>(tg + 8 * c);
+          const float4 t1 = *reinterpret_cast<const float4*>(tg + 8 * c + 4);
+          t[0] = t0.x; t[1] = t0.y; t[2] = t0.z; t[3] = t0.w;
+          t[4] = t1.x; t[5] = t1.y; t[6] = t1.z; t[7] = t1.w;
+        }
         const uint32_t* hp = &hv[i].x;
-        const uint32_t* gp = &gv.x;
         uint4 r;
         uint32_t* rp = &r.x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float s0 = bf16_lo(ou[e]), s1 = bf16_hi(ou[e]);
           if (MODE == 2) {
-            s0 = __fmul_rn(tanhf(bf16_lo(gp[e])), s0);
-            s1 = __fmul_rn(tanhf(bf16_hi(gp[e])), s1);
+            s0 = __fmul_rn(t[2 * e], s0);
+            s1 = __fmul_rn(t[2 * e + 1], s1);
           }
           rp[e] = pack_bf16x2(__fadd_rn(bf16_lo(hp[e]), s0), __fadd_rn(bf16_hi(hp[e]), s1));
         }
@@ -204,14 +210,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 
 hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const uint16_t* w,
                              uint16_t* y, long long ldy, uint16_t* h, long long ldh,
-                             const uint16_t* gate, int rows, int D, float eps,
+                             const float* tg, int rows, int D, float eps,
                              hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   const int nch = D / 8;
   if (D % 8 != 0 || nch > 64 * 16 || mode < 0 || mode > 3) return hipErrorInvalidValue;
 #define MING_RMS_M(LPR, CPL, MODE)                                                \
   hipLaunchKernelGGL((rmsnorm_kernel<LPR, CPL, MODE>), dim3((rows + rpb - 1) / rpb), \
-                     dim3(256), 0, s, x, ldx, w, y, ldy, h, ldh, gate, rows, D, eps)
+                     dim3(256), 0, s, x, ldx, w, y, ldy, h, ldh, tg, rows, D, eps)
 #define MING_RMS(LPR, CPL)                                                     \
   do {                                                                         \
     const int rpb = 4 * (64 / (LPR));                                          \

@@ -553,6 +553,14 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
           reinterpret_cast<uint2*>(yp)[0] = make_uint2(v.x, v.y);
           reinterpret_cast<uint2*>(yp)[1] = make_uint2(v.z, v.w);
         }
+        if (a.yh) {
+          uint4 f;
+          f.x = bf16x2_to_f16x2(v.x);
+          f.y = bf16x2_to_f16x2(v.y);
+          f.z = bf16x2_to_f16x2(v.z);
+          f.w = bf16x2_to_f16x2(v.w);
+          *reinterpret_cast<uint4*>(a.yh + (long long)m * a.ldyh + n) = f;
+        }
       }
     }
   }

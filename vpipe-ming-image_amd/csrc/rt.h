@@ -40,10 +40,13 @@ int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ld
 int rt_ffn_xh(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
               const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
               int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh);
-// h = bf16(h + tanh(gate) * rmsnorm(sub)) (gate NULL: h + rmsnorm(sub)), sub
-// left as it was: ming_rmsnorm in place followed by ming_gated_residual /
-// ming_residual_add.
+// h = bf16(h + tgate * rmsnorm(sub)) with tgate = tanh(gate) from
+// rt_tanh_gates (tgate NULL: h + rmsnorm(sub)), sub left as it was:
+// ming_rmsnorm in place followed by ming_gated_residual / ming_residual_add.
 int rt_norm_residual(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
-                     int64_t lds, const uint16_t* w, const uint16_t* gate, int rows, int D,
+                     int64_t lds, const uint16_t* w, const float* tgate, int rows, int D,
                      float eps);
+// t[0, n) = tanh(mods[n, 2n)), t[n, 2n) = tanh(mods[3n, 4n)) in f32: a block's
+// two residual gates, once per block instead of once per element.
+int rt_tanh_gates(ming_ctx* c, const uint16_t* mods, int n, float* t);
 }  // namespace ming

@@ -71,6 +71,8 @@ struct ming_ctx {
   size_t scratch_bytes = 0;
   void* xh = nullptr;          // fp16 copy of the projection input
   size_t xh_bytes = 0;
+  void* xh2 = nullptr;         // fp16 copy of the SwiGLU output (w2's input)
+  size_t xh2_bytes = 0;
   void* vt = nullptr;          // V^T [heads][128][keys] for attention
   size_t vt_bytes = 0;
   void* up = nullptr;          // general route + SwiGLU: the projection before the gate
@@ -276,6 +278,19 @@ int ensure_xh(ming_ctx* c, size_t bytes) {
   return MING_OK;
 }
 
+int ensure_xh2(ming_ctx* c, size_t bytes) {
+  if (bytes <= c->xh2_bytes) return MING_OK;
+  MING_HIP(hipStreamSynchronize(c->stream), "scratch grow sync");
+  if (c->xh2) (void)hipFree(c->xh2);
+  c->xh2 = nullptr;
+  c->xh2_bytes = 0;
+  size_t want = std::max(bytes, (size_t)1 << 20);
+  if (hipMalloc(&c->xh2, want) != hipSuccess)
+    return fail(MING_ERR_ALLOC, "fp16 activation scratch allocation failed");
+  c->xh2_bytes = want;
+  return MING_OK;
+}
+
 int ensure_vt(ming_ctx* c, size_t bytes) {
   if (bytes <= c->vt_bytes) return MING_OK;
   MING_HIP(hipStreamSynchronize(c->stream), "scratch grow sync");
@@ -397,6 +412,7 @@ int ming_ctx_destroy(ming_ctx* c) {
   (void)hipStreamSynchronize(c->stream);
   if (c->scratch) (void)hipFree(c->scratch);
   if (c->xh) (void)hipFree(c->xh);
+  if (c->xh2) (void)hipFree(c->xh2);
   if (c->vt) (void)hipFree(c->vt);
   if (c->up) (void)hipFree(c->up);
   if (c->part) (void)hipFree(c->part);
@@ -710,13 +726,15 @@ int ming_qweight_lora_rank(const ming_qweight* q, int segment, int slot) {
 }
 
 // The projection with its options: `gate` fuses SwiGLU into the output
-// (y = bf16(silu(gate) * bf16(lin(x)))), `xh_ready` says the context's fp16
-// copy of x already holds this x (the fast route then skips its conversion),
-// and *took_fast reports whether the fast route ran.
+// (y = bf16(silu(gate) * bf16(lin(x)))); `xh_src`, when set, is an fp16 copy
+// of this x with row stride K that the fast route reads instead of converting
+// x itself; `yh`, when set, receives an fp16 copy of the output (row stride
+// N) from the fast route's epilogue; *took_fast reports whether the fast
+// route ran (only then was `yh` written).
 static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
                     int64_t ldx, uint16_t* y, int64_t ldy, int M,
                     const float* scales, const uint16_t* gate, int64_t ldg,
-                    bool xh_ready, bool* took_fast) {
+                    const uint16_t* xh_src, bool* took_fast, uint16_t* yh = nullptr) {
   if (took_fast) *took_fast = false;
   if (!c || !qc || !x || !y) return fail(MING_ERR_ARG, "ming_lin: null argument");
   if (qc->ctx != c) return fail(MING_ERR_ARG, "ming_lin: weight of another context");
@@ -852,9 +870,10 @@ static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
   }
   qa.t = T; qa.ldt = t_cols > 0 ? t_cols : 0; qa.nseg = nseg;
   qa.g = nullptr; qa.ldg = 0;
+  qa.yh = nullptr; qa.ldyh = 0;
   if (fast) {
     // The fast route reads x as fp16 carrying the same (bf16) values.
-    if (!xh_ready) {
+    if (!xh_src) {
       int rc = ensure_xh(c, (size_t)M * q->K * 2);
       if (rc != MING_OK) return rc;
       uint16_t* xh = (uint16_t*)c->xh;
@@ -863,8 +882,10 @@ static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
                                                               q->K, c->stream); }),
                "bf16->fp16 launch");
     }
-    qa.x = (const uint16_t*)c->xh; qa.ldx = q->K; qa.codes = q->codes_f; qa.sb = q->sbf;
+    qa.x = xh_src ? xh_src : (const uint16_t*)c->xh;
+    qa.ldx = q->K; qa.codes = q->codes_f; qa.sb = q->sbf;
     qa.g = gate; qa.ldg = ldg;       // the fast epilogue fuses SwiGLU
+    qa.yh = yh; qa.ldyh = q->N;      // and writes the fp16 copy the next projection reads
   }
   const double base_flops = 2.0 * M * (double)q->N * q->K;
   double tail_flops = 0.0;
@@ -908,14 +929,14 @@ static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
 int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
              int64_t ldx, uint16_t* y, int64_t ldy, int M,
              const float* scales) {
-  return lin_impl(c, qc, x, ldx, y, ldy, M, scales, nullptr, 0, false, nullptr);
+  return lin_impl(c, qc, x, ldx, y, ldy, M, scales, nullptr, 0, nullptr, nullptr);
 }
 
 int ming_lin_swiglu(ming_ctx* c, const ming_qweight* w, const uint16_t* x,
                     int64_t ldx, const uint16_t* g, int64_t ldg, uint16_t* out,
                     int64_t ldo, int M, const float* scales) {
   if (!g) return fail(MING_ERR_ARG, "ming_lin_swiglu: null gate");
-  return lin_impl(c, w, x, ldx, out, ldo, M, scales, g, ldg, false, nullptr);
+  return lin_impl(c, w, x, ldx, out, ldo, M, scales, g, ldg, nullptr, nullptr);
 }
 
 // gpu_ff; xh_ready: the context's fp16 copy already holds x (row stride H).
@@ -930,13 +951,23 @@ static int ffn_impl(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
     return fail(MING_ERR_SHAPE, "ming_ffn: need w1, w3 [ffn][H] and w2 [H][ffn]");
   if (ldh < F || ldh % 8 != 0 || !aligned(h, 16))
     return fail(MING_ERR_SHAPE, "ming_ffn: h needs ldh >= ffn, ldh % 8 == 0, 16-byte alignment");
-  bool fast1 = false;
-  int rc = lin_impl(c, w1, x, ldx, h, ldh, M, scales, nullptr, 0, xh_ready, &fast1);
+  bool fast1 = false, fast3 = false;
+  int rc = lin_impl(c, w1, x, ldx, h, ldh, M, scales, nullptr, 0,
+                    xh_ready ? (const uint16_t*)c->xh : nullptr, &fast1);
   if (rc != MING_OK) return rc;
-  // w3 reads the same x: the fp16 copy w1's fast route made serves it too
-  rc = lin_impl(c, w3, x, ldx, h, ldh, M, scales, h, ldh, xh_ready || fast1, nullptr);
+  // w3 reads the same x: the fp16 copy w1's fast route made serves it too.
+  // Its epilogue also writes the fp16 copy of h that w2 reads, into a buffer
+  // of its own (w3's other tiles still read x from the first).
+  if (M > 0) {
+    rc = ensure_xh2(c, (size_t)M * F * 2);
+    if (rc != MING_OK) return rc;
+  }
+  rc = lin_impl(c, w3, x, ldx, h, ldh, M, scales, h, ldh,
+                (xh_ready || fast1) ? (const uint16_t*)c->xh : nullptr, &fast3,
+                (uint16_t*)c->xh2);
   if (rc != MING_OK) return rc;
-  return lin_impl(c, w2, h, ldh, y, ldy, M, scales, nullptr, 0, false, nullptr);
+  return lin_impl(c, w2, h, ldh, y, ldy, M, scales, nullptr, 0,
+                  fast3 ? (const uint16_t*)c->xh2 : nullptr, nullptr);
 }
 
 int ming_ffn(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
@@ -950,7 +981,7 @@ int ming_ffn(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
 // residual h += (tanh(gate) *) y.
 static int rms_impl(ming_ctx* c, int mode, const uint16_t* x, int64_t ldx,
                     const uint16_t* w, uint16_t* y, int64_t ldy, uint16_t* h,
-                    int64_t ldh, const uint16_t* gate, int rows, int D, float eps,
+                    int64_t ldh, const float* gate, int rows, int D, float eps,
                     const char* who) {
   if (!c || !x || !w || (mode <= 1 && !y) || (mode >= 2 && !h) || (mode == 2 && !gate))
     return fail(MING_ERR_ARG, std::string(who) + ": null argument");
@@ -970,7 +1001,7 @@ static int rms_impl(ming_ctx* c, int mode, const uint16_t* x, int64_t ldx,
     h = (uint16_t*)c->xh;
     ldh = D;
   }
-  const double bytes = (mode == 0 ? 4.0 : 6.0) * rows * D + (mode == 2 ? 4.0 : 2.0) * D;
+  const double bytes = (mode == 0 ? 4.0 : 6.0) * rows * D + (mode == 2 ? 6.0 : 2.0) * D;
   MING_HIP(profiled(c, mode >= 2 ? kBNormRes : kBRms, 0.0, bytes,
                     [&] { return ming::launch_rmsnorm_ex(mode, x, ldx, w, y, ldy, h, ldh,
                                                          gate, rows, D, eps, c->stream); }),
@@ -1337,15 +1368,25 @@ int rt_rmsnorm_f16(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* 
 }
 
 int rt_norm_residual(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
-                     int64_t lds, const uint16_t* w, const uint16_t* gate, int rows, int D,
+                     int64_t lds, const uint16_t* w, const float* tgate, int rows, int D,
                      float eps) {
-  return rms_impl(c, gate ? 2 : 3, sub, lds, w, nullptr, 0, h, ldh, gate, rows, D, eps,
+  return rms_impl(c, tgate ? 2 : 3, sub, lds, w, nullptr, 0, h, ldh, tgate, rows, D, eps,
                   "post-norm residual");
+}
+
+int rt_tanh_gates(ming_ctx* c, const uint16_t* mods, int n, float* t) {
+  DeviceGuard g(c->device);
+  MING_HIP(profiled(c, kBModulate, 0.0, 2.0 * 2 * n + 4.0 * 2 * n,
+                    [&] { return ming::launch_tanh_gates(mods, n, t, c->stream); }),
+           "tanh gates launch");
+  c->eng.elementwise += 1;
+  return ok();
 }
 
 int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ldx,
               uint16_t* y, int64_t ldy, int M, const float* scales) {
-  return lin_impl(c, qw, x, ldx, y, ldy, M, scales, nullptr, 0, true, nullptr);
+  return lin_impl(c, qw, x, ldx, y, ldy, M, scales, nullptr, 0, (const uint16_t*)c->xh,
+                  nullptr);
 }
 
 int rt_ffn_xh(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
