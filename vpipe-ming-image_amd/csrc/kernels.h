@@ -83,10 +83,14 @@ hipError_t validate_attention_kernels();
 
 // T[m][c] = bf16(coef[c/16] * sum_k x[m][k] A[row(c)][k]) for c < n_cols,
 // row(c) = 16*grp[c/16] + c%16 (grp -1: a zero column). A is [R][K] bf16.
+// Up to this many projections share one x.A launch (q, k, v; w1, w3).
+constexpr int kMaxXaSources = 4;
 struct LoraXaArgs {
   const uint16_t* x;
   long long ldx;
-  const uint16_t* A;
+  // A stacks [rows][K]: group entry g reads rows 16 * (g & 4095) + 0..15 of
+  // A[g >> 12]; a negative entry is a zero (padding) group
+  const uint16_t* A[kMaxXaSources];
   int K;
   int M;
   int n_cols;           // multiple of 64

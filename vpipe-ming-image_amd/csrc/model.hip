@@ -116,9 +116,11 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
   // ---- attention half ----
   // the norm also writes the fp16 copy q, k and v read (one conversion, not three)
   RC(ming::rt_rmsnorm_f16(c, x, H, g1, w.nrm, H, rows, H, eps));
-  RC(ming::rt_lin_xh(c, b->q, w.nrm, H, w.qkv, 3 * H, rows, scales));
-  RC(ming::rt_lin_xh(c, b->k, w.nrm, H, w.qkv + H, 3 * H, rows, scales));
-  RC(ming::rt_lin_xh(c, b->v, w.nrm, H, w.qkv + 2 * H, 3 * H, rows, scales));
+  {
+    const ming_qweight* qkv[3] = {b->q, b->k, b->v};
+    uint16_t* out[3] = {w.qkv, w.qkv + H, w.qkv + 2 * H};
+    RC(ming::rt_lin3_xh(c, qkv, w.nrm, H, out, 3 * H, rows, scales));
+  }
   RC(ming_qk_norm_rope(c, w.qkv, 3 * H, 0, H, rows, NH, 128, b->nq, b->nk, cos_t, sin_t,
                        eps));
   // the attention output reuses the normed-input plane (its q/k/v are done)

@@ -340,7 +340,10 @@ __global__ __launch_bounds__(256, 2) void lora_xa_kernel(const LoraXaArgs a) {
     const int c = c0 + pr + 32 * i;
     const int g = a.grp[c >> 4];
     azero[i] = g < 0;
-    arow[i] = a.A + (long long)(g < 0 ? 0 : (16 * g + (c & 15))) * a.K + pc * 8;
+    // a padding group reads (and zeroes) rows of the first live group's stack
+    const int gs = g < 0 ? a.grp[0] : g;
+    arow[i] = a.A[gs >> 12] + (long long)(g < 0 ? 0 : (16 * (g & 4095) + (c & 15))) * a.K +
+              pc * 8;
   }
   uint4 xr[4], ar[2];
   auto load = [&](int kt) {

@@ -623,11 +623,14 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
     m = m < mlast ? m : mlast;
     xoff[i] = (uint32_t)(((long long)m * a.ldx + 8 * c) * 2);
   }
-  // A rows: stacked column col -> row 16 * grp[col / 16] + col % 16; padding
-  // groups (and columns past n_cols) read the first live group's rows
-  // (finite; their T columns are exactly 0 or never written)
+  // A rows: stacked column col -> row 16 * (g & 4095) + col % 16 of stack
+  // A[g >> 12], g = grp[col / 16]; padding groups (and columns past n_cols)
+  // read the first live group's rows (finite; their T columns are exactly 0
+  // or never written). One DMA instruction covers 8 columns of one 16-group,
+  // so its stack (its scalar base) is uniform across the wave.
   const int g_safe = a.grp[0];
   uint32_t aoff[4];
+  int asrc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int p = 64 * (4 * wave + i) + lane;
@@ -635,8 +638,10 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
     const int c = (p & 7) ^ ((r >> 1) & 7);
     const int col = c0 + r;
     const int g = col < a.n_cols ? a.grp[col >> 4] : -1;
-    const int row = g < 0 ? 16 * g_safe : 16 * g + (col & 15);
+    const int gs = g < 0 ? g_safe : g;
+    const int row = 16 * (gs & 4095) + (g < 0 ? 0 : (col & 15));
     aoff[i] = (uint32_t)(((long long)row * a.K + 8 * c) * 2);
+    asrc[i] = __builtin_amdgcn_readfirstlane(gs >> 12);
   }
   auto issue_grp = [&](int g, int kt, const uint4* S) {
     if (g < 2) {
@@ -645,10 +650,10 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
       for (int i = 4 * g; i < 4 * g + 4; ++i)
         dma16_sb(base, xoff[i], lds_addr(S + 64 * (8 * wave + i)));
     } else {
-      const void* base = a.A + (long long)kt * 64;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        dma16_sb(base, aoff[i], lds_addr(S + 2048 + 64 * (4 * wave + i)));
+        dma16_sb(a.A[asrc[i]] + (long long)kt * 64, aoff[i],
+                 lds_addr(S + 2048 + 64 * (4 * wave + i)));
     }
   };
 
@@ -869,8 +874,13 @@ hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The K split depends on M and K only (sized for one projection's stack of
+// about 3 column blocks), never on how many columns are stacked: each T
+// column is then summed in the same order, and so has the same bits, whether
+// its projection's x.A runs alone or stacked with others over the same x.
 int lora_xa_fast_slices(int M, int n_cols, int K) {
-  const int tiles = ((M + 255) / 256) * ((n_cols + 127) / 128);
+  (void)n_cols;
+  const int tiles = ((M + 255) / 256) * 3;
   const int KT = K / 64;
   int ks = 256 / (tiles > 0 ? tiles : 1);       // about one round of the chip
   const int kmax = KT / 8 > 1 ? KT / 8 : 1;      // keep >= 8 K steps per slice

@@ -37,6 +37,10 @@ int rt_rmsnorm_f16(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* 
                    uint16_t* y, int64_t ldy, int rows, int D, float eps);
 int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ldx,
               uint16_t* y, int64_t ldy, int M, const float* scales);
+// the three projections q, k, v over the same normed x, one x.A launch for
+// their adapters, outputs y[i] with one row stride
+int rt_lin3_xh(ming_ctx* c, const ming_qweight* const* qw, const uint16_t* x, int64_t ldx,
+               uint16_t* const* y, int64_t ldy, int M, const float* scales);
 int rt_ffn_xh(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
               const ming_qweight* w2, const uint16_t* x, int64_t ldx, uint16_t* y,
               int64_t ldy, int M, const float* scales, uint16_t* h, int64_t ldh);

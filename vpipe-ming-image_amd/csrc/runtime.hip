@@ -725,92 +725,121 @@ int ming_qweight_lora_rank(const ming_qweight* q, int segment, int slot) {
   return q->segs[segment].slot[slot].rank;
 }
 
-// The projection with its options: `gate` fuses SwiGLU into the output
-// (y = bf16(silu(gate) * bf16(lin(x)))); `xh_src`, when set, is an fp16 copy
-// of this x with row stride K that the fast route reads instead of converting
-// x itself; `yh`, when set, receives an fp16 copy of the output (row stride
-// N) from the fast route's epilogue; *took_fast reports whether the fast
-// route ran (only then was `yh` written).
-static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
-                    int64_t ldx, uint16_t* y, int64_t ldy, int M,
-                    const float* scales, const uint16_t* gate, int64_t ldg,
-                    const uint16_t* xh_src, bool* took_fast, uint16_t* yh = nullptr) {
-  if (took_fast) *took_fast = false;
-  if (!c || !qc || !x || !y) return fail(MING_ERR_ARG, "ming_lin: null argument");
-  if (qc->ctx != c) return fail(MING_ERR_ARG, "ming_lin: weight of another context");
-  ming_qweight* q = const_cast<ming_qweight*>(qc);
+// One projection's output side: y [M][ldy]; `gate` fuses SwiGLU into the
+// output (y = bf16(silu(gate) * bf16(lin(x)))); `yh`, when set, receives an
+// fp16 copy of the output (row stride N) from the fast route's epilogue;
+// *took_fast reports whether the fast route ran (only then was `yh` written).
+struct LinOut {
+  uint16_t* y = nullptr;
+  int64_t ldy = 0;
+  const uint16_t* gate = nullptr;
+  int64_t ldg = 0;
+  uint16_t* yh = nullptr;
+  bool* took_fast = nullptr;
+};
+
+// n projections over the same x [M][K] (q, k, v; w1, w3): x is converted to
+// fp16 once for all of them (`xh_src`, when set, is that copy already made,
+// row stride K), and every live adapter of every one of them goes into ONE
+// stacked x.A launch -- the stacks' 16-rank groups side by side in T, group
+// entries naming their weight -- before each projection's GEMM reads its own
+// columns of T. n == 1 is lin() (ming-dit.cc:1763-1771).
+static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const LinOut* outs,
+                     const uint16_t* x, int64_t ldx, int M, const float* scales,
+                     const uint16_t* xh_src) {
+  for (int i = 0; i < n; ++i)
+    if (outs[i].took_fast) *outs[i].took_fast = false;
+  if (!c || !x || n < 1 || n > ming::kMaxXaSources)
+    return fail(MING_ERR_ARG, "ming_lin: null argument");
   if (M < 0) return fail(MING_ERR_ARG, "ming_lin: M < 0");
-  if (ldx < q->K || ldy < q->N || ldx % 8 != 0 || ldy % 4 != 0)
-    return fail(MING_ERR_SHAPE,
-                "ming_lin: need ldx >= K, ldx % 8 == 0, ldy >= N, ldy % 4 == 0");
-  if (!aligned(x, 16) || !aligned(y, 8))
-    return fail(MING_ERR_ARG, "ming_lin: x must be 16-byte and y 8-byte aligned");
-  if (gate && (ldg < q->N || ldg % 8 != 0 || !aligned(gate, 16) || ldy % 8 != 0 ||
-               !aligned(y, 16)))
-    return fail(MING_ERR_SHAPE,
-                "ming_lin_swiglu: gate and output need strides % 8 == 0 and 16-byte "
-                "alignment (ldg >= N)");
+  if (!aligned(x, 16)) return fail(MING_ERR_ARG, "ming_lin: x must be 16-byte and y 8-byte aligned");
+  const int K = qs[0] ? qs[0]->K : 0;
+  for (int i = 0; i < n; ++i) {
+    const ming_qweight* q = qs[i];
+    const LinOut& o = outs[i];
+    if (!q || !o.y) return fail(MING_ERR_ARG, "ming_lin: null argument");
+    if (q->ctx != c) return fail(MING_ERR_ARG, "ming_lin: weight of another context");
+    if (q->K != K) return fail(MING_ERR_SHAPE, "ming_lin: projections over one x need one K");
+    if (ldx < q->K || o.ldy < q->N || ldx % 8 != 0 || o.ldy % 4 != 0)
+      return fail(MING_ERR_SHAPE,
+                  "ming_lin: need ldx >= K, ldx % 8 == 0, ldy >= N, ldy % 4 == 0");
+    if (!aligned(o.y, 8))
+      return fail(MING_ERR_ARG, "ming_lin: x must be 16-byte and y 8-byte aligned");
+    if (o.gate && (o.ldg < q->N || o.ldg % 8 != 0 || !aligned(o.gate, 16) || o.ldy % 8 != 0 ||
+                   !aligned(o.y, 16)))
+      return fail(MING_ERR_SHAPE,
+                  "ming_lin_swiglu: gate and output need strides % 8 == 0 and 16-byte "
+                  "alignment (ldg >= N)");
+  }
   if (M == 0) return ok();
   DeviceGuard g(c->device);
 
-  // The live stack, per segment, in slot order.
-  ming::QprojArgs qa{};
+  // The live stacks, per weight and segment, in slot order.
+  ming::QprojArgs qa[ming::kMaxXaSources] = {};
   ming::LoraXaArgs xa{};
-  const int nseg = (int)q->segs.size();
-  int xa_groups = 0;   // 16-wide groups of T over all segments
-  int qp_groups = 0;
-  bool any_live = false;
-  for (int si = 0; si < nseg; ++si)
-    for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl)
-      if (q->segs[si].slot[sl].rank > 0 && scales && scales[sl] != 0.0f)
-        any_live = true;
-  if (any_live) {
-    int rc = build_stacks(q);
-    if (rc != MING_OK) return rc;
-  }
-  uint64_t lora_flops = 0;
-  int live_segs = 0;
-  for (int si = 0; si < nseg; ++si) {
-    const Segment& sg = q->segs[si];
-    ming::QprojSeg& d = qa.seg[si];
-    d.n_begin = sg.n_begin;
-    d.n_end = sg.n_begin + sg.N;
-    d.t_col0 = xa_groups * 16;
-    d.grp0 = qp_groups;
-    d.chunks = 0;
-    d.ldb = any_live ? q->b_ld[si] : 0;
-    d.B = any_live ? q->B_seg[si] : nullptr;
-    int seg_groups = 0;
-    for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
-      const LoraBind& b = sg.slot[sl];
-      if (b.rank <= 0 || !scales || scales[sl] == 0.0f) continue;
-      const int ar = q->a_row0[si * MING_MAX_LORA_SLOTS + sl];
-      const int bc = q->b_col0[si * MING_MAX_LORA_SLOTS + sl];
-      for (int gi = 0; gi < b.rank16 / 16; ++gi) {
-        if (xa_groups + seg_groups >= ming::kMaxGroups ||
-            qp_groups + seg_groups >= ming::kMaxGroups)
-          return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
-        xa.grp[xa_groups + seg_groups] = (int16_t)(ar / 16 + gi);
-        xa.coef[xa_groups + seg_groups] = b.fold * scales[sl];
-        qa.grp[qp_groups + seg_groups] = (int16_t)(bc / 16 + gi);
-        ++seg_groups;
+  int xa_groups = 0;   // 16-wide groups of T over every weight and segment
+  uint64_t lora_flops[ming::kMaxXaSources] = {};
+  int live_segs[ming::kMaxXaSources] = {};
+  double xa_flops = 0.0, tail_flops[ming::kMaxXaSources] = {};
+  bool xa_fits = true;
+  for (int i = 0; i < n; ++i) {
+    ming_qweight* q = const_cast<ming_qweight*>(qs[i]);
+    const int nseg = (int)q->segs.size();
+    bool any_live = false;
+    for (int si = 0; si < nseg; ++si)
+      for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl)
+        if (q->segs[si].slot[sl].rank > 0 && scales && scales[sl] != 0.0f) any_live = true;
+    if (any_live) {
+      int rc = build_stacks(q);
+      if (rc != MING_OK) return rc;
+      xa.A[i] = q->A_all;
+      if ((uint64_t)q->a_rows * (uint64_t)q->K * 2 > (1ull << 32)) xa_fits = false;
+    }
+    int qp_groups = 0;
+    for (int si = 0; si < nseg; ++si) {
+      const Segment& sg = q->segs[si];
+      ming::QprojSeg& d = qa[i].seg[si];
+      d.n_begin = sg.n_begin;
+      d.n_end = sg.n_begin + sg.N;
+      d.t_col0 = xa_groups * 16;
+      d.grp0 = qp_groups;
+      d.chunks = 0;
+      d.ldb = any_live ? q->b_ld[si] : 0;
+      d.B = any_live ? q->B_seg[si] : nullptr;
+      int seg_groups = 0;
+      for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
+        const LoraBind& b = sg.slot[sl];
+        if (b.rank <= 0 || !scales || scales[sl] == 0.0f) continue;
+        const int ar = q->a_row0[si * MING_MAX_LORA_SLOTS + sl];
+        const int bc = q->b_col0[si * MING_MAX_LORA_SLOTS + sl];
+        for (int gi = 0; gi < b.rank16 / 16; ++gi) {
+          if (xa_groups + seg_groups >= ming::kMaxGroups ||
+              qp_groups + seg_groups >= ming::kMaxGroups)
+            return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
+          xa.grp[xa_groups + seg_groups] = (int16_t)((i << 12) | (ar / 16 + gi));
+          xa.coef[xa_groups + seg_groups] = b.fold * scales[sl];
+          qa[i].grp[qp_groups + seg_groups] = (int16_t)(bc / 16 + gi);
+          ++seg_groups;
+        }
+        lora_flops[i] += 2ull * (uint64_t)M * (uint64_t)b.rank * (uint64_t)(q->K + sg.N);
+        xa_flops += 2.0 * M * b.rank * (double)q->K;
+        tail_flops[i] += 2.0 * M * b.rank * (double)sg.N;
       }
-      lora_flops += 2ull * (uint64_t)M * (uint64_t)b.rank * (uint64_t)(q->K + sg.N);
+      if (seg_groups == 0) continue;
+      ++live_segs[i];
+      // pad the segment's T columns to whole 64-wide chunks with zero groups
+      const int padded = round_up(seg_groups, 4);
+      for (int gi = seg_groups; gi < padded; ++gi) {
+        if (xa_groups + gi >= ming::kMaxGroups || qp_groups + gi >= ming::kMaxGroups)
+          return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
+        xa.grp[xa_groups + gi] = -1;
+        xa.coef[xa_groups + gi] = 0.0f;
+        qa[i].grp[qp_groups + gi] = -1;
+      }
+      d.chunks = padded / 4;
+      xa_groups += padded;
+      qp_groups += padded;
     }
-    if (seg_groups == 0) continue;
-    ++live_segs;
-    // pad the segment's T columns to whole 64-wide chunks with zero groups
-    const int padded = round_up(seg_groups, 4);
-    for (int gi = seg_groups; gi < padded; ++gi) {
-      if (xa_groups + gi >= ming::kMaxGroups || qp_groups + gi >= ming::kMaxGroups)
-        return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
-      xa.grp[xa_groups + gi] = -1;
-      xa.coef[xa_groups + gi] = 0.0f;
-      qa.grp[qp_groups + gi] = -1;
-    }
-    d.chunks = padded / 4;
-    xa_groups += padded;
-    qp_groups += padded;
   }
   const int t_cols = xa_groups * 16;
   uint16_t* T = nullptr;
@@ -818,30 +847,24 @@ static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
     int rc = ensure_scratch(c, (size_t)M * t_cols * 2);
     if (rc != MING_OK) return rc;
     T = (uint16_t*)c->scratch;
-    xa.x = x; xa.ldx = ldx; xa.A = q->A_all; xa.K = q->K; xa.M = M;
+    xa.x = x; xa.ldx = ldx; xa.K = K; xa.M = M;
     xa.n_cols = t_cols; xa.t = T; xa.ldt = t_cols;
-    double xa_flops = 0.0;
-    for (int si = 0; si < nseg; ++si)
-      for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
-        const LoraBind& b = q->segs[si].slot[sl];
-        if (b.rank > 0 && scales && scales[sl] != 0.0f)
-          xa_flops += 2.0 * M * b.rank * (double)q->K;
-      }
-    // the fast x.A addresses x and the A stack as 64-bit bases plus 32-bit
+    // the fast x.A addresses x and each A stack as 64-bit bases plus 32-bit
     // byte offsets
     const bool xa_fast = c->route != MING_ROUTE_GENERAL && ldx % 8 == 0 &&
-                         (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) &&
-                         (uint64_t)q->a_rows * (uint64_t)q->K * 2 <= (1ull << 32);
+                         (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) && xa_fits;
     int ks = 1;
     if (xa_fast) {
-      ks = ming::lora_xa_fast_slices(M, t_cols, q->K);
+      ks = ming::lora_xa_fast_slices(M, t_cols, K);
       if (ks > 1) {
-        int rc = ensure_part(c, (size_t)ks * M * t_cols * 4);
+        rc = ensure_part(c, (size_t)ks * M * t_cols * 4);
         if (rc != MING_OK) return rc;
       }
     }
-    MING_HIP(profiled(c, kBXa, xa_flops,
-                      2.0 * M * q->K + 2.0 * t_cols * (double)q->K + 2.0 * M * t_cols,
+    double a_bytes = 0.0;
+    for (int i = 0; i < n; ++i)
+      if (xa.A[i]) a_bytes += 2.0 * qs[i]->a_rows * (double)K;
+    MING_HIP(profiled(c, kBXa, xa_flops, 2.0 * M * K + a_bytes + 2.0 * M * t_cols,
                       [&] {
                         return xa_fast ? ming::launch_lora_xa_fast(xa, (float*)c->part,
                                                                    ks, c->stream)
@@ -850,80 +873,101 @@ static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
              "lora_xa launch");
     c->eng.lora_xa += 1;
   }
-  // The fast route addresses each operand as a 64-bit base plus 32-bit
-  // byte offsets: x (fp16 copy, row stride K), T and every B stack must fit.
-  bool fits32 = (uint64_t)M * (uint64_t)q->K * 2 <= (1ull << 32) &&
-                (uint64_t)M * (uint64_t)t_cols * 2 <= (1ull << 32);
-  for (int si = 0; si < nseg && t_cols > 0; ++si)
-    if (qa.seg[si].chunks > 0 &&
-        (uint64_t)q->segs[si].N * (uint64_t)q->b_ld[si] * 2 > (1ull << 32))
-      fits32 = false;
-  const bool fast = q->bits != 16 && q->fast && c->route != MING_ROUTE_GENERAL && fits32;
-  qa.x = x; qa.ldx = ldx; qa.codes = q->codes_t; qa.sb = q->sb; qa.w16 = q->w16;
-  qa.y = y; qa.ldy = ldy; qa.M = M; qa.N = q->N; qa.K = q->K;
-  if (gate && !fast) {
-    // the general route writes the projection first: into a plane of its
-    // own, since y may be the gate itself
-    int rc = ensure_up(c, (size_t)M * q->N * 2);
+  // Which projections take the fast route. It addresses each operand as a
+  // 64-bit base plus 32-bit byte offsets: x (fp16 copy, row stride K), T and
+  // every B stack must fit.
+  bool fast[ming::kMaxXaSources] = {};
+  bool any_fast = false;
+  for (int i = 0; i < n; ++i) {
+    const ming_qweight* q = qs[i];
+    bool fits32 = (uint64_t)M * (uint64_t)K * 2 <= (1ull << 32) &&
+                  (uint64_t)M * (uint64_t)t_cols * 2 <= (1ull << 32);
+    for (int si = 0; si < (int)q->segs.size() && t_cols > 0; ++si)
+      if (qa[i].seg[si].chunks > 0 &&
+          (uint64_t)q->segs[si].N * (uint64_t)q->b_ld[si] * 2 > (1ull << 32))
+        fits32 = false;
+    fast[i] = q->bits != 16 && q->fast && c->route != MING_ROUTE_GENERAL && fits32;
+    any_fast = any_fast || fast[i];
+  }
+  // The fast route reads x as fp16 carrying the same (bf16) values: one
+  // conversion serves every projection here.
+  const uint16_t* xh = xh_src;
+  if (any_fast && !xh) {
+    int rc = ensure_xh(c, (size_t)M * K * 2);
     if (rc != MING_OK) return rc;
-    qa.y = (uint16_t*)c->up; qa.ldy = q->N;
+    uint16_t* dst = (uint16_t*)c->xh;
+    MING_HIP(profiled(c, kBCvt, 0.0, 4.0 * M * K,
+                      [&] { return ming::launch_bf16_to_f16(x, ldx, dst, K, M, K,
+                                                            c->stream); }),
+             "bf16->fp16 launch");
+    xh = dst;
   }
-  qa.t = T; qa.ldt = t_cols > 0 ? t_cols : 0; qa.nseg = nseg;
-  qa.g = nullptr; qa.ldg = 0;
-  qa.yh = nullptr; qa.ldyh = 0;
-  if (fast) {
-    // The fast route reads x as fp16 carrying the same (bf16) values.
-    if (!xh_src) {
-      int rc = ensure_xh(c, (size_t)M * q->K * 2);
+  for (int i = 0; i < n; ++i) {
+    const ming_qweight* q = qs[i];
+    const LinOut& o = outs[i];
+    ming::QprojArgs& a = qa[i];
+    a.x = x; a.ldx = ldx; a.codes = q->codes_t; a.sb = q->sb; a.w16 = q->w16;
+    a.y = o.y; a.ldy = o.ldy; a.M = M; a.N = q->N; a.K = K;
+    a.t = T; a.ldt = t_cols > 0 ? t_cols : 0; a.nseg = (int)q->segs.size();
+    a.g = nullptr; a.ldg = 0;
+    a.yh = nullptr; a.ldyh = 0;
+    if (o.gate && !fast[i]) {
+      // the general route writes the projection first: into a plane of its
+      // own, since y may be the gate itself
+      int rc = ensure_up(c, (size_t)M * q->N * 2);
       if (rc != MING_OK) return rc;
-      uint16_t* xh = (uint16_t*)c->xh;
-      MING_HIP(profiled(c, kBCvt, 0.0, 4.0 * M * q->K,
-                        [&] { return ming::launch_bf16_to_f16(x, ldx, xh, q->K, M,
-                                                              q->K, c->stream); }),
-               "bf16->fp16 launch");
+      a.y = (uint16_t*)c->up; a.ldy = q->N;
     }
-    qa.x = xh_src ? xh_src : (const uint16_t*)c->xh;
-    qa.ldx = q->K; qa.codes = q->codes_f; qa.sb = q->sbf;
-    qa.g = gate; qa.ldg = ldg;       // the fast epilogue fuses SwiGLU
-    qa.yh = yh; qa.ldyh = q->N;      // and writes the fp16 copy the next projection reads
-  }
-  const double base_flops = 2.0 * M * (double)q->N * q->K;
-  double tail_flops = 0.0;
-  for (int si = 0; si < nseg; ++si)
-    for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl) {
-      const LoraBind& b = q->segs[si].slot[sl];
-      if (b.rank > 0 && scales && scales[sl] != 0.0f)
-        tail_flops += 2.0 * M * b.rank * (double)q->segs[si].N;
+    if (fast[i]) {
+      a.x = xh; a.ldx = K; a.codes = q->codes_f; a.sb = q->sbf;
+      a.g = o.gate; a.ldg = o.ldg;     // the fast epilogue fuses SwiGLU
+      a.yh = o.yh; a.ldyh = q->N;      // and writes the fp16 copy the next projection reads
     }
-  const double wbytes = q->bits == 16
-                            ? 2.0 * q->N * q->K
-                            : (double)q->N * q->K * q->bits / 8 + 4.0 * q->N * (q->K / 64);
-  const int bk = fast ? (q->bits == 4 ? kBF4 : kBF8)
-                      : (q->bits == 4 ? kBQ4 : (q->bits == 8 ? kBQ8 : kBDense));
-  MING_HIP(profiled(c, bk, base_flops + tail_flops,
-                    2.0 * M * q->K + wbytes + 2.0 * M * q->N,
-                    [&] {
-                      return fast ? ming::launch_qproj_fast(q->bits, qa, c->stream)
-                                  : ming::launch_qproj(q->bits, qa, c->stream);
-                    }),
-           "qproj launch");
-  if (gate && !fast) {
-    // the general route writes the projection; SwiGLU follows in place
-    MING_HIP(profiled(c, kBSwiglu, 0.0, 6.0 * M * q->N,
-                      [&] { return ming::launch_swiglu(gate, ldg, (const uint16_t*)c->up,
-                                                       q->N, y, ldy, M, q->N,
-                                                       c->stream); }),
-             "swiglu launch");
+    const double base_flops = 2.0 * M * (double)q->N * K;
+    const double wbytes = q->bits == 16
+                              ? 2.0 * q->N * K
+                              : (double)q->N * K * q->bits / 8 + 4.0 * q->N * (K / 64);
+    const int bk = fast[i] ? (q->bits == 4 ? kBF4 : kBF8)
+                           : (q->bits == 4 ? kBQ4 : (q->bits == 8 ? kBQ8 : kBDense));
+    MING_HIP(profiled(c, bk, base_flops + tail_flops[i],
+                      2.0 * M * K + wbytes + 2.0 * M * q->N,
+                      [&] {
+                        return fast[i] ? ming::launch_qproj_fast(q->bits, a, c->stream)
+                                       : ming::launch_qproj(q->bits, a, c->stream);
+                      }),
+             "qproj launch");
+    if (o.gate && !fast[i]) {
+      // the general route writes the projection; SwiGLU follows
+      MING_HIP(profiled(c, kBSwiglu, 0.0, 6.0 * M * q->N,
+                        [&] { return ming::launch_swiglu(o.gate, o.ldg, (const uint16_t*)c->up,
+                                                         q->N, o.y, o.ldy, M, q->N,
+                                                         c->stream); }),
+               "swiglu launch");
+    }
+    if (o.gate) c->eng.elementwise += 1;
+    if (o.took_fast) *o.took_fast = fast[i];
+    if (fast[i]) c->eng.gemm_fast += 1;
+    if (q->bits == 4) c->eng.gemm_q4 += 1;
+    else if (q->bits == 8) c->eng.gemm_q8 += 1;
+    else c->eng.gemm_dense += 1;
+    c->eng.lora_proj += live_segs[i];
+    c->eng.gemm_flops += 2ull * (uint64_t)M * (uint64_t)q->N * (uint64_t)K + lora_flops[i];
   }
-  if (gate) c->eng.elementwise += 1;
-  if (took_fast) *took_fast = fast;
-  if (fast) c->eng.gemm_fast += 1;
-  if (q->bits == 4) c->eng.gemm_q4 += 1;
-  else if (q->bits == 8) c->eng.gemm_q8 += 1;
-  else c->eng.gemm_dense += 1;
-  c->eng.lora_proj += live_segs;
-  c->eng.gemm_flops += 2ull * (uint64_t)M * (uint64_t)q->N * (uint64_t)q->K + lora_flops;
   return ok();
+}
+
+// One projection (see LinOut, lin_multi).
+static int lin_impl(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
+                    int64_t ldx, uint16_t* y, int64_t ldy, int M,
+                    const float* scales, const uint16_t* gate, int64_t ldg,
+                    const uint16_t* xh_src, bool* took_fast, uint16_t* yh = nullptr) {
+  if (!qc) {
+    if (took_fast) *took_fast = false;
+    return fail(MING_ERR_ARG, "ming_lin: null argument");
+  }
+  LinOut o;
+  o.y = y; o.ldy = ldy; o.gate = gate; o.ldg = ldg; o.yh = yh; o.took_fast = took_fast;
+  return lin_multi(c, 1, &qc, &o, x, ldx, M, scales, xh_src);
 }
 
 int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
@@ -951,20 +995,22 @@ static int ffn_impl(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
     return fail(MING_ERR_SHAPE, "ming_ffn: need w1, w3 [ffn][H] and w2 [H][ffn]");
   if (ldh < F || ldh % 8 != 0 || !aligned(h, 16))
     return fail(MING_ERR_SHAPE, "ming_ffn: h needs ldh >= ffn, ldh % 8 == 0, 16-byte alignment");
-  bool fast1 = false, fast3 = false;
-  int rc = lin_impl(c, w1, x, ldx, h, ldh, M, scales, nullptr, 0,
-                    xh_ready ? (const uint16_t*)c->xh : nullptr, &fast1);
-  if (rc != MING_OK) return rc;
-  // w3 reads the same x: the fp16 copy w1's fast route made serves it too.
-  // Its epilogue also writes the fp16 copy of h that w2 reads, into a buffer
-  // of its own (w3's other tiles still read x from the first).
+  // w1 and w3 read the same x: one fp16 conversion and one x.A launch for
+  // both. w3's epilogue fuses the SwiGLU (gate = w1's output, in place) and
+  // writes the fp16 copy of h that w2 reads, into a buffer of its own (w3's
+  // other tiles still read x from the first).
   if (M > 0) {
-    rc = ensure_xh2(c, (size_t)M * F * 2);
+    int rc = ensure_xh2(c, (size_t)M * F * 2);
     if (rc != MING_OK) return rc;
   }
-  rc = lin_impl(c, w3, x, ldx, h, ldh, M, scales, h, ldh,
-                (xh_ready || fast1) ? (const uint16_t*)c->xh : nullptr, &fast3,
-                (uint16_t*)c->xh2);
+  bool fast3 = false;
+  const ming_qweight* pair[2] = {w1, w3};
+  LinOut outs[2];
+  outs[0].y = h; outs[0].ldy = ldh;
+  outs[1].y = h; outs[1].ldy = ldh; outs[1].gate = h; outs[1].ldg = ldh;
+  outs[1].yh = (uint16_t*)c->xh2; outs[1].took_fast = &fast3;
+  int rc = lin_multi(c, 2, pair, outs, x, ldx, M, scales,
+                     xh_ready ? (const uint16_t*)c->xh : nullptr);
   if (rc != MING_OK) return rc;
   return lin_impl(c, w2, h, ldh, y, ldy, M, scales, nullptr, 0,
                   fast3 ? (const uint16_t*)c->xh2 : nullptr, nullptr);
@@ -1387,6 +1433,16 @@ int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ld
               uint16_t* y, int64_t ldy, int M, const float* scales) {
   return lin_impl(c, qw, x, ldx, y, ldy, M, scales, nullptr, 0, (const uint16_t*)c->xh,
                   nullptr);
+}
+
+int rt_lin3_xh(ming_ctx* c, const ming_qweight* const* qw, const uint16_t* x, int64_t ldx,
+               uint16_t* const* y, int64_t ldy, int M, const float* scales) {
+  LinOut outs[3];
+  for (int i = 0; i < 3; ++i) {
+    outs[i].y = y[i];
+    outs[i].ldy = ldy;
+  }
+  return lin_multi(c, 3, qw, outs, x, ldx, M, scales, (const uint16_t*)c->xh);
 }
 
 int rt_ffn_xh(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
