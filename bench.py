@@ -37,8 +37,8 @@ PEAK_TFLOPS = 2500.0          # MI355X dense fp16/bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
-def live_rank():
-    return sum(r for r, s in zip(RANKS, SCALES) if s != 0.0)
+def live_rank(ranks=RANKS, scales=SCALES):
+    return sum(r for r, s in zip(ranks, scales) if s != 0.0)
 
 
 def ffn_flops(M):
@@ -122,11 +122,11 @@ def cpu_baseline(hosts, x_host, target_s, threads):
                       f"{dt:.1f} s"}
 
 
-def forward_flops(img, cap):
+def forward_flops(img, cap, ranks=RANKS, scales=SCALES):
     """Algorithmic FLOP of one 34-block forward (GEMM + live LoRA +
     attention): 2 context-refiner blocks over the caption, 2 noise-refiner
     blocks over the image, 30 layers over the joint sequence."""
-    R = live_rank()
+    R = live_rank(ranks, scales)
     JT = img + cap
     per_row = 2 * (4 * HID * HID + 3 * HID * FFN)          # q,k,v,o,w1,w3,w2
     lora_row = 2 * R * (4 * (HID + HID) + 3 * (HID + FFN))
@@ -135,26 +135,31 @@ def forward_flops(img, cap):
     return rows * (per_row + lora_row) + attn
 
 
-def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2):
-    """A 34-block w4g64 model with random-init weights (quantized on the GPU by
-    the library's pack writer), the config-2 adapter set bound on all seven
-    projections of every block, dense embedders and final layer."""
+def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2, bits=4,
+                        ranks=RANKS):
+    """A 34-block w{bits}g64 model with random-init weights (quantized on the
+    GPU by the library's pack writer), an adapter of each rank in `ranks`
+    bound on all seven projections of every block (slot i = ranks[i]; the
+    config-2 set by default), dense embedders and final layer. The model's
+    projection weights are listed in model.projections."""
     dev = "cuda"
     keep = []
+    projections = []
 
     def qw(N, K):
         w = torch.randn((N, K), generator=gen, device=dev) * 0.02
-        codes = torch.empty((N, K // 8), dtype=torch.int32, device=dev)
+        codes = torch.empty((N, K * bits // 32), dtype=torch.int32, device=dev)
         sc = torch.empty((N, K // 64), dtype=torch.int16, device=dev)
         bi = torch.empty((N, K // 64), dtype=torch.int16, device=dev)
         torch.cuda.synchronize()
-        ctx.quantize_pack(w, N, K, 4, codes, sc, bi)
+        ctx.quantize_pack(w, N, K, bits, codes, sc, bi)
         ctx.synchronize()
-        q = m.QWeight.quantized(ctx, codes, sc, bi, 4, on_device=True)
+        q = m.QWeight.quantized(ctx, codes, sc, bi, bits, on_device=True)
         return q
 
     def lora(q, N, K):
-        for slot, r in enumerate(RANKS):
+        projections.append(q)
+        for slot, r in enumerate(ranks):
             A = (torch.randn((r, K), generator=gen, device=dev) / K ** 0.5
                  ).to(torch.bfloat16).view(torch.int16)
             B = (torch.randn((N, r), generator=gen, device=dev) * 0.01
@@ -212,7 +217,84 @@ def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2):
           "final_lin_b": vec(64, 0.0, 0.05)}
     for k, v in tw.items():
         setattr(d, k, m._h(v))
-    return m.Model(ctx, d, cb, mb, keep=keep + [tw, cb, mb])
+    model = m.Model(ctx, d, cb, mb, keep=keep + [tw, cb, mb])
+    model.projections = projections
+    return model
+
+
+def layout_2048():
+    """Positions of the 2048^2 joint sequence: a 128 x 128 patch grid (16384
+    image tokens) at t = 257, then 256 caption rows at (1 + i, 0, 0)."""
+    import numpy as np
+    img, cap, grid = 16384, 256, 128
+    pt = np.concatenate([np.full(img, cap + 1), 1 + np.arange(cap)]).astype(np.int32)
+    ph = np.concatenate([np.arange(img) // grid, np.zeros(cap)]).astype(np.int32)
+    pw = np.concatenate([np.arange(img) % grid, np.zeros(cap)]).astype(np.int32)
+    return img, cap, (pt, ph, pw)
+
+
+def run_forward2048(ctx, m, torch, gen, steps):
+    """the 34-block w4 forward at 2048^2 with the config-2 adapters
+    on all 238 modules; ms per forward after two untimed ones."""
+    model = build_forward_model(ctx, m, torch, gen)
+    model.set_caption_cache(False)
+    for i, sc in enumerate(SCALES):
+        model.set_lora_scale(i, sc)
+    img, cap, pos = layout_2048()
+    lat = torch.randn((img, 64), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    capt = torch.randn((cap, 2560), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    out = torch.empty((img, 64), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(2):
+        model.forward(lat, capt, 2560, img, cap, cap, *pos, 0.5, out)
+    each = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        model.forward(lat, capt, 2560, img, cap, cap, *pos, 0.5, out)
+        each.append((time.perf_counter() - t0) * 1e3)
+    model.close()
+    flops = forward_flops(img, cap)
+    med = sorted(each)[len(each) // 2]
+    return {"metric": "34-block w4g64 forward @2048^2 (configs[3])", "value": round(med, 2),
+            "unit": "ms", "higher_is_better": False, "ms_each": [round(t, 2) for t in each],
+            "tflops": round(flops / (med * 1e-3) / 1e12, 2),
+            "forward_tflop": round(flops / 1e12, 2), "tokens": img + cap}
+
+
+def run_cfg2048(ctx, m, torch, gen, steps=11):
+    """classifier-free guidance at 2048^2, w8g64, eight r64 slots
+    with strengths uniform in [-1, 1.5], `steps` denoise steps (a positive and a
+    zero-negative forward each) on the shift-6 schedule; the per-forward ms and
+    the sustained TFLOP/s."""
+    import numpy as np
+    ranks = (64,) * 8
+    rng = np.random.default_rng(5)
+    scales = tuple(float(v) for v in rng.uniform(-1.0, 1.5, 8))
+    model = build_forward_model(ctx, m, torch, gen, bits=8, ranks=ranks)
+    for i, sc in enumerate(scales):
+        model.set_lora_scale(i, sc)
+    img, cap, pos = layout_2048()
+    capt = torch.randn((cap, 2560), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    lat = (torch.randn((img, 64), generator=gen, device="cuda")).float().cpu().numpy()
+    torch.cuda.synchronize()
+    # one untimed step first (workspaces, both caption cache entries)
+    warm = lat.copy()
+    model.denoise(warm, capt, 2560, cap, cap, pos, img, 1, 6.0, 4.0)
+    marks = [time.perf_counter()]
+    model.denoise(lat, capt, 2560, cap, cap, pos, img, steps, 6.0, 4.0,
+                  progress=lambda i, n: marks.append(time.perf_counter()) or True)
+    model.close()
+    per_step = [(b - a) * 1e3 for a, b in zip(marks, marks[1:])]
+    flops = 2 * forward_flops(img, cap, ranks, scales)      # positive + negative
+    total_s = (marks[-1] - marks[0])
+    med = sorted(per_step)[len(per_step) // 2]
+    return {"metric": "CFG x2 w8g64 denoise @2048^2 (configs[4])",
+            "value": round(flops * steps / total_s / 1e12, 2), "unit": "TFLOP/s sustained",
+            "higher_is_better": True, "steps": steps, "guidance": 4.0,
+            "ms_per_step_each": [round(t, 1) for t in per_step],
+            "ms_per_forward_median": round(med / 2, 2),
+            "step_tflop": round(flops / 1e12, 2), "lora_scales": [round(v, 3) for v in scales],
+            "finite": bool(np.isfinite(lat).all())}
 
 
 def time_forward(ctx, m, torch, gen, steps, warmup):
@@ -322,6 +404,9 @@ def main():
     ap.add_argument("--no-forward", action="store_true",
                     help="skip the 34-block forward at 1024^2")
     ap.add_argument("--forward-steps", type=int, default=5)
+    ap.add_argument("--workload", choices=("ffn", "forward2048", "cfg2048"), default="ffn",
+                    help="ffn: the headline line (configs[1] + the 1024^2 forward); "
+                         "forward2048: configs[3]; cfg2048: configs[4]")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB device-to-device three times (the "
                          "known-size kernel the HBM byte counters are scaled by)")
@@ -348,6 +433,14 @@ def main():
     stream = torch.cuda.Stream()
     ctx = m.Ctx(0, stream.cuda_stream)
     gen = torch.Generator(device="cuda").manual_seed(2)
+    if args.workload != "ffn":
+        fn = run_forward2048 if args.workload == "forward2048" else run_cfg2048
+        res = fn(ctx, m, torch, gen, args.forward_steps) if args.workload == "forward2048" \
+            else fn(ctx, m, torch, gen)
+        res.update({"n_gpus": 1, "data": "synthetic", "dtype": "w4/w8 g64 -> fp16 MFMA"})
+        ctx.close()
+        print(json.dumps(res))
+        return
     (w1, w3, w2), hosts, x = build(ctx, m, torch, gen)
     M = M_TOK
     g = torch.empty((M, FFN), dtype=torch.int16, device="cuda")
