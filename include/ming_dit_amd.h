@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MING_ABI_VERSION 2
+#define MING_ABI_VERSION 3
 
 /* Runtime-LoRA slots: lora::Stack::kMax (ming-dit.h:117) and the eight
  * `lora`..`lora8` keys (ming-model-config-stage.h:37-56). */
@@ -64,12 +64,15 @@ typedef struct ming_engagement {
   uint64_t gemm_flops;  /* 2*M*N*K + sum_live 2*M*r*(K+N) per projection */
   int64_t gemm_fast;    /* of the quantized projections, those on the fast route */
   int64_t cap_cache_hits; /* forwards whose caption path came from the caption cache */
+  int64_t gemv;           /* of the projections, those run as a GEMV (M <= 8, no live adapter) */
 } ming_engagement;
 
 /* Kernel routes for quantized projections. AUTO takes the fast route
  * (fp16 activations, DMA-fed LDS ring, fragment dequant) whenever the
- * weight's scales and biases are exact in fp16; GENERAL always takes the
- * general kernel. Both compute the same function to the same bar. */
+ * weight's scales and biases are exact in fp16, and a GEMV (each weight
+ * streamed once, f32 dot products) for M <= 8 rows with no live adapter, as
+ * the adaLN and timestep projections run at M = 1. GENERAL always takes the
+ * general kernel. All compute the same function to the same bar. */
 enum { MING_ROUTE_AUTO = 0, MING_ROUTE_GENERAL = 1 };
 
 /* Per-launch kernel timing (HIP events around each launch, on the

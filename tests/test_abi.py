@@ -18,7 +18,7 @@ def test_library_exports_every_header_symbol():
 
 
 def test_abi_version():
-    assert m.lib().ming_abi_version() == 2
+    assert m.lib().ming_abi_version() == 3
 
 
 def test_null_arguments_are_refused_with_a_reason():

@@ -152,6 +152,23 @@ hipError_t launch_quantize(const float* w, int N, int K, int bits,
                            uint32_t* codes, uint16_t* scales, uint16_t* biases,
                            hipStream_t s);
 
+// ---- projections over a handful of rows (gemv.hip) ----------------------------
+// y[m][n] = bf16(sum_k x[m][k] W[n][k]) for m < M <= kGemvMaxM, W in the
+// resident general layout (codes + sb for bits 4/8, w16 for bits 16).
+constexpr int kGemvMaxM = 8;
+struct GemvArgs {
+  const uint16_t* x;
+  long long ldx;
+  const uint32_t* codes;
+  const uint32_t* sb;
+  const uint16_t* w16;
+  uint16_t* y;
+  long long ldy;
+  int M, N, K;
+};
+hipError_t launch_gemv(int bits, const GemvArgs& a, hipStream_t s);
+hipError_t validate_gemv_kernels();
+
 // ---- the fast quantized route (qproj_fast.hip) --------------------------------
 // x is fp16 (carrying bf16 values), a.codes / a.sb the fast resident layout.
 hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s);

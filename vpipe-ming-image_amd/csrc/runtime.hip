@@ -94,13 +94,13 @@ namespace {
 // marks, ming-dit.cc:1689-1717, as HIP events around each launch).
 enum Bucket {
   kBQ4, kBQ8, kBDense, kBF4, kBF8, kBCvt, kBXa, kBRms, kBQkRope, kBRopeTab, kBSwiglu, kBResid,
-  kBModulate, kBBias, kBLn, kBQuant, kBAttn, kBNormRes, kBCount
+  kBModulate, kBBias, kBLn, kBQuant, kBAttn, kBNormRes, kBGemv, kBCount
 };
 const char* const kBucketName[kBCount] = {
     "qproj.w4", "qproj.w8", "qproj.dense", "qproj_fast.w4", "qproj_fast.w8",
     "cvt_f16", "lora_xa", "rmsnorm",
     "qk_norm_rope", "rope_table", "swiglu", "residual", "modulate",
-    "bias_act", "ln_modulate", "quantize", "attention", "norm_residual"};
+    "bias_act", "ln_modulate", "quantize", "attention", "norm_residual", "gemv"};
 
 hipEvent_t take_event(ming_ctx* c) {
   if (!c->pool.empty()) {
@@ -381,6 +381,7 @@ int ming_ctx_create(int device, void* hip_stream, ming_ctx** out) {
   if (e == hipSuccess) e = ming::validate_norm_kernels();
   if (e == hipSuccess) e = ming::validate_elementwise_kernels();
   if (e == hipSuccess) e = ming::validate_qproj_fast_kernels();
+  if (e == hipSuccess) e = ming::validate_gemv_kernels();
   if (e == hipSuccess) e = ming::validate_attention_kernels();
   if (e != hipSuccess)
     return fail(MING_ERR_KERNEL,
@@ -773,6 +774,40 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
   }
   if (M == 0) return ok();
   DeviceGuard g(c->device);
+
+  // A handful of rows and no live adapter (the adaLN and timestep
+  // projections run at M = 1): the GEMV streams each weight once instead of
+  // running a 256-row tile.
+  if (c->route == MING_ROUTE_AUTO && M <= ming::kGemvMaxM) {
+    bool gemv = true;
+    for (int i = 0; i < n && gemv; ++i) {
+      const ming_qweight* q = qs[i];
+      if (outs[i].gate || outs[i].yh) gemv = false;
+      for (const Segment& sg : q->segs)
+        for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl)
+          if (sg.slot[sl].rank > 0 && scales && scales[sl] != 0.0f) gemv = false;
+    }
+    if (gemv) {
+      for (int i = 0; i < n; ++i) {
+        const ming_qweight* q = qs[i];
+        const ming::GemvArgs ga{x, ldx, q->codes_t, q->sb, q->w16, outs[i].y, outs[i].ldy,
+                                M, q->N, K};
+        const double wbytes = q->bits == 16
+                                  ? 2.0 * q->N * K
+                                  : (double)q->N * K * q->bits / 8 + 4.0 * q->N * (K / 64);
+        MING_HIP(profiled(c, kBGemv, 2.0 * M * (double)q->N * K,
+                          wbytes + 2.0 * M * K + 2.0 * M * q->N,
+                          [&] { return ming::launch_gemv(q->bits, ga, c->stream); }),
+                 "gemv launch");
+        if (q->bits == 4) c->eng.gemm_q4 += 1;
+        else if (q->bits == 8) c->eng.gemm_q8 += 1;
+        else c->eng.gemm_dense += 1;
+        c->eng.gemv += 1;
+        c->eng.gemm_flops += 2ull * (uint64_t)M * (uint64_t)q->N * (uint64_t)K;
+      }
+      return ok();
+    }
+  }
 
   // The live stacks, per weight and segment, in slot order.
   ming::QprojArgs qa[ming::kMaxXaSources] = {};

@@ -35,7 +35,7 @@ class Engagement(C.Structure):
                 ("qk_norm_rope", C.c_int64), ("rope_table", C.c_int64),
                 ("attention", C.c_int64), ("elementwise", C.c_int64),
                 ("gemm_flops", C.c_uint64), ("gemm_fast", C.c_int64),
-                ("cap_cache_hits", C.c_int64)]
+                ("cap_cache_hits", C.c_int64), ("gemv", C.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
