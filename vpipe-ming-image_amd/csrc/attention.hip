@@ -21,14 +21,17 @@
 //                   half h holding keys 8h..8h+7 of each slice in
 //                   consecutive registers -- exactly the B operand layout
 //                   of the P.V MFMA, so P never leaves registers.
-//   online softmax  exp2 domain (logits pre-multiplied by scale*log2 e),
-//                   running max exchanged across lane halves, running
-//                   sums kept per lane half and combined at the end.
+//   online softmax  exp2 domain (scale*log2 e folded into the exp2
+//                   argument), a lazily moved reference max exchanged
+//                   across lane halves, running sums kept per lane half
+//                   and combined at the end.
 //   O^T += V^T.P^T  4 d-tiles x 4 key slices, P rounded to bf16 (the
 //                   reference's steel kernel also feeds P as the input
 //                   type to its second GEMM). V^T rows are fed in the same
 //                   swapped order, so each lane ends holding 8 consecutive
 //                   d of its query: 16-byte token-major stores.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -85,6 +88,10 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const uint4*>(qp + 16 * s);
   }
+  // Wait for them here (vmcnt(0); expcnt, lgkmcnt open): the compiler then
+  // puts no wait for them into the key loop, where a vmcnt wait would also
+  // wait for the ring's DMA of the next tile, every step.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 
   // DMA offsets (bytes from the step's base). K: chunk p -> row p >> 4,
   // logical chunk (p & 15) ^ (row & 15). V^T: chunk p -> row p >> 3,
@@ -123,52 +130,79 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
   for (int u = 0; u < 4; ++u)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[u][r] = 0.0f;
-  float mrun = -INFINITY, lrun = 0.0f;
+  // Lazy online softmax (exp2 domain): P = exp2(sl2 * s - mref) against a
+  // reference max mref that moves only when some query's max rises more
+  // than kLazy above it, so P <= 2^kLazy and O and l are rescaled only then
+  // (a wave-uniform branch), not at every key block.
+  constexpr float kLazy = 8.0f;
+  float mref = -INFINITY, lrun = 0.0f;
   const float sl2 = a.sl2;
 
-  auto step = [&](int kb, const uint4* SK, const uint4* SV) {
-    // When R < 64 the (single) block was loaded from row 0; otherwise the
-    // last block was shifted back to R - 64: keys are then offset.
+  // MASK: the last key block, which may be shifted back to stay inside
+  // [0, R) and may hold keys past R; every other block runs unmasked.
+  auto step = [&](auto mask_tag, int kb, const uint4* SK, const uint4* SV) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int kstart = kb * ABK;
-    const int kmax = R - ABK;
-    const int kload = kstart < kmax ? kstart : (kmax > 0 ? kmax : 0);
-    const int shift = kstart - kload;      // 0 except for a shifted last block
+    int shift = 0;
+    if constexpr (MASK) {
+      // When R < 64 the (single) block was loaded from row 0; otherwise the
+      // last block was shifted back to R - 64: keys are then offset.
+      const int kmax = R - ABK;
+      const int kload = kstart < kmax ? kstart : (kmax > 0 ? kmax : 0);
+      shift = kstart - kload;
+    }
     floatx16_t sacc[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[t][r] = 0.0f;
+    // the two key tiles alternate, so consecutive MFMAs never chain on one
+    // accumulator
+    int rr[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int row = 32 * t + swap23(fr) + shift;   // K row in the loaded tile
-      const int rr = row < ABK ? row : ABK - 1;
+      rr[t] = 32 * t + swap23(fr);                    // K row in the loaded tile
+      if constexpr (MASK) {
+        rr[t] += shift;
+        rr[t] = rr[t] < ABK ? rr[t] : ABK - 1;
+      }
+    }
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const uint4 kf = SK[16 * rr + ((2 * s + fh) ^ (rr & 15))];
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint4 kf = SK[16 * rr[t] + ((2 * s + fh) ^ (rr[t] & 15))];
         sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, kf), __builtin_bit_cast(bf16x8_t, qf[s]),
             sacc[t], 0, 0, 0);
       }
-    }
     // register r of tile t holds key 32t + 16(r/8) + 8fh + (r%8)
-    const bool tail = kstart + ABK > R;
+    if constexpr (MASK) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kstart + 32 * t + 16 * (r >> 3) + 8 * fh + (r & 7);
+          sacc[t][r] = key < R ? sacc[t][r] : -INFINITY;
+        }
+    }
     float mloc = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = sacc[t][r] * sl2;
-        if (tail) {
-          const int key = kstart + 32 * t + 16 * (r >> 3) + 8 * fh + (r & 7);
-          x = key < R ? x : -INFINITY;
-        }
-        sacc[t][r] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    mloc = fmaxf(mloc, xor32(mloc));
-    const float mnew = fmaxf(mrun, mloc);
-    const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
-    mrun = mnew;
+      for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[t][r]);
+    mloc = fmaxf(mloc, xor32(mloc)) * sl2;            // sl2 > 0: max commutes
+    if (__any(mloc > mref + kLazy)) {
+      const float mnew = fmaxf(mref, mloc);
+      const float alpha = __builtin_amdgcn_exp2f(mref - mnew);
+      mref = mnew;
+      lrun *= alpha;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[u][r] *= alpha;
+    }
+    const float nm = -mref;
     float psum = 0.0f;
     uint4 pf[4];
 #pragma unroll
@@ -177,7 +211,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
       float p[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        p[e] = __builtin_amdgcn_exp2f(sacc[t][r0 + e] - mnew);
+        p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r0 + e], sl2, nm));
         psum += p[e];
       }
       pf[j].x = pack_bf16x2_rne(p[0], p[1]);
@@ -185,35 +219,34 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
       pf[j].z = pack_bf16x2_rne(p[4], p[5]);
       pf[j].w = pack_bf16x2_rne(p[6], p[7]);
     }
-    lrun = lrun * alpha + psum;
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[u][r] *= alpha;
+    lrun += psum;
     // O^T[d][q] += V^T[d][k] P^T[k][q]; V^T row fed for output row i is
-    // d = 32u + swap23(i)
+    // d = 32u + swap23(i). The four d-tiles alternate (no accumulator chain).
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int vrow = 32 * u + swap23(fr);
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int u = 0; u < 4; ++u) {
+        const int vrow = 32 * u + swap23(fr);
         const uint4 vf = SV[vrow * 8 + ((2 * j + fh) ^ ((vrow >> 1) & 7))];
         oacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, vf), __builtin_bit_cast(bf16x8_t, pf[j]),
             oacc[u], 0, 0, 0);
       }
-    }
   };
+  const std::integral_constant<bool, false> whole{};
+  const std::integral_constant<bool, true> last{};
 
   issue(0, sk0, sv0);
   for (int kb = 0; kb < NKB; kb += 2) {
     attn_sync();                                   // stage kb landed; sk1/sv1 free
     issue(kb + 1 < NKB ? kb + 1 : NKB - 1, sk1, sv1);
-    step(kb, sk0, sv0);
+    if (kb + 1 < NKB) step(whole, kb, sk0, sv0);
+    else step(last, kb, sk0, sv0);
     if (kb + 1 >= NKB) break;
     attn_sync();
     issue(kb + 2 < NKB ? kb + 2 : NKB - 1, sk0, sv0);
-    step(kb + 1, sk1, sv1);
+    if (kb + 2 < NKB) step(whole, kb + 1, sk1, sv1);
+    else step(last, kb + 1, sk1, sv1);
   }
   attn_sync();                                     // no DMA outlives the block
 
