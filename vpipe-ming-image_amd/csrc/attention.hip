@@ -167,15 +167,31 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
         rr[t] = rr[t] < ABK ? rr[t] : ABK - 1;
       }
     }
+    // The 16 K fragments of the step, read 4 ahead of their MFMAs (pinned;
+    // the scheduler alone keeps about 2 in flight).
+    uint4 kfa[16];
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint4 kf = SK[16 * rr[t] + ((2 * s + fh) ^ (rr[t] & 15))];
+      for (int t = 0; t < 2; ++t)
+        kfa[2 * s + t] = SK[16 * rr[t] + ((2 * s + fh) ^ (rr[t] & 15))];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
         sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8_t, kf), __builtin_bit_cast(bf16x8_t, qf[s]),
+            __builtin_bit_cast(bf16x8_t, kfa[2 * s + t]), __builtin_bit_cast(bf16x8_t, qf[s]),
             sacc[t], 0, 0, 0);
-      }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int g = 0; g < 16 - 4; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_barrier(0);
     // register r of tile t holds key 32t + 16(r/8) + 8fh + (r%8)
     if constexpr (MASK) {
 #pragma unroll

@@ -34,7 +34,7 @@ namespace {
 // the residual, so each is bit-identical to rmsnorm followed by the separate
 // residual / conversion kernel.
 template <int LPR, int CPL, int MODE>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(
+__global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
     const uint16_t* x, long long ldx, const uint16_t* __restrict__ w,
     uint16_t* y, long long ldy, uint16_t* h, long long ldh,
     const float* __restrict__ tg, int rows, int D, float eps) {
@@ -45,13 +45,25 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   const int nch = D >> 3;
   const bool live = row < rows;
   const uint16_t* xr = x + (long long)(live ? row : 0) * ldx;
-  uint4 v[CPL];
+  // Every load of the row is issued before the reduction: the row, and the
+  // norm weight (MODE <= 1) or the residual row (MODE >= 2); the weight
+  // of the residual modes is read after it, which keeps their registers
+  // inside 5 waves per SIMD (4352 rows of 3840 then fit one round).
+  uint4 v[CPL], hv[CPL], wv[CPL];
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = sub + LPR * i;
     if (live && c < nch) {
       v[i] = *reinterpret_cast<const uint4*>(xr + 8 * c);
+      if constexpr (MODE <= 1) wv[i] = *reinterpret_cast<const uint4*>(w + 8 * c);
+      else hv[i] = *reinterpret_cast<const uint4*>(h + (long long)row * ldh + 8 * c);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = sub + LPR * i;
+    if (live && c < nch) {
       const uint32_t* u = &v[i].x;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -65,22 +77,13 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
   const float inv = 1.0f / sqrtf(ss / (float)D + eps);
   if (!live) return;
-  uint4 hv[CPL];
-  if (MODE >= 2) {  // the residual stream, loaded before any store of this row
-    const uint16_t* hr = h + (long long)row * ldh;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = sub + LPR * i;
-      if (c < nch) hv[i] = *reinterpret_cast<const uint4*>(hr + 8 * c);
-    }
-  }
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = sub + LPR * i;
     if (c < nch) {
-      const uint4 wv = *reinterpret_cast<const uint4*>(w + 8 * c);
+      if constexpr (MODE >= 2) wv[i] = *reinterpret_cast<const uint4*>(w + 8 * c);
       const uint32_t* u = &v[i].x;
-      const uint32_t* wu = &wv.x;
+      const uint32_t* wu = &wv[i].x;
       uint4 o;
       uint32_t* ou = &o.x;
 #pragma unroll
