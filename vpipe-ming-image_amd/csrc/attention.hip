@@ -281,6 +281,15 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
         v.z = pack_bf16x2_rne(oacc[u][8 * hh + 4] * inv, oacc[u][8 * hh + 5] * inv);
         v.w = pack_bf16x2_rne(oacc[u][8 * hh + 6] * inv, oacc[u][8 * hh + 7] * inv);
         *reinterpret_cast<uint4*>(op + 32 * u + 16 * hh) = v;
+        if (a.oh) {
+          uint4 f;
+          f.x = bf16x2_to_f16x2(v.x);
+          f.y = bf16x2_to_f16x2(v.y);
+          f.z = bf16x2_to_f16x2(v.z);
+          f.w = bf16x2_to_f16x2(v.w);
+          *reinterpret_cast<uint4*>(a.oh + (long long)q * a.ldoh + head * AHD + 8 * fh +
+                                    32 * u + 16 * hh) = f;
+        }
       }
   }
 }

@@ -74,6 +74,10 @@ struct AttnArgs {
   int ldv;
   uint16_t* o;
   long long ldo;
+  // optional fp16 copy of O (the same bf16 values), [R][NH*128] at ldoh: the
+  // fast projection route's input for the o-projection
+  uint16_t* oh;
+  long long ldoh;
   int R, NH;
   float sl2;
 };

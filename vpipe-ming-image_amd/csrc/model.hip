@@ -123,10 +123,11 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
   }
   RC(ming_qk_norm_rope(c, w.qkv, 3 * H, 0, H, rows, NH, 128, b->nq, b->nk, cos_t, sin_t,
                        eps));
-  // the attention output reuses the normed-input plane (its q/k/v are done)
-  RC(ming_attention(c, w.qkv, 3 * H, 0, H, 2 * H, w.nrm, H, rows, NH, 128,
-                    1.0f / std::sqrt(128.0f)));
-  RC(ming_lin(c, b->o, w.nrm, H, w.ob, H, rows, scales));
+  // the attention output reuses the normed-input plane (its q/k/v are done);
+  // its fp16 copy is the o-projection's input
+  RC(ming::rt_attention_xh(c, w.qkv, 3 * H, 0, H, 2 * H, w.nrm, H, rows, NH,
+                           1.0f / std::sqrt(128.0f)));
+  RC(ming::rt_lin_xh(c, b->o, w.nrm, H, w.ob, H, rows, scales));
   // post-norm and the (gated) residual in one pass
   RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->an2, modulated ? w.tg : nullptr, rows, H,
                             eps));

@@ -37,6 +37,11 @@ int rt_rmsnorm_f16(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* 
                    uint16_t* y, int64_t ldy, int rows, int D, float eps);
 int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ldx,
               uint16_t* y, int64_t ldy, int M, const float* scales);
+// ming_attention that also leaves the fp16 copy of its output in the
+// context's plane, for rt_lin_xh over that output (the o-projection)
+int rt_attention_xh(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int k_col,
+                    int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
+                    float scale);
 // the three projections q, k, v over the same normed x, one x.A launch for
 // their adapters, outputs y[i] with one row stride
 int rt_lin3_xh(ming_ctx* c, const ming_qweight* const* qw, const uint16_t* x, int64_t ldx,

@@ -1145,9 +1145,11 @@ int ming_qk_norm_rope(ming_ctx* c, uint16_t* x, int64_t ld, int q_col, int k_col
   return ok();
 }
 
-int ming_attention(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int k_col,
-                   int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
-                   int head_dim, float scale) {
+// oh: optional fp16 copy of the output (the context's xh plane, row stride
+// n_heads * 128) for the o-projection's fast route.
+static int attention_impl(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int k_col,
+                          int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
+                          int head_dim, float scale, bool fp16_copy) {
   if (!c || !qkv || !out) return fail(MING_ERR_ARG, "ming_attention: null argument");
   if (head_dim != 128)
     return fail(MING_ERR_SHAPE, "ming_attention: head_dim must be 128");
@@ -1173,6 +1175,12 @@ int ming_attention(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int 
   a.k = qkv + k_col; a.ldk = ld;
   a.vt = (const uint16_t*)c->vt; a.ldv = ldv;
   a.o = out; a.ldo = ldo;
+  if (fp16_copy) {
+    rc = ensure_xh(c, (size_t)rows * w * 2);
+    if (rc != MING_OK) return rc;
+    a.oh = (uint16_t*)c->xh;
+    a.ldoh = w;
+  }
   a.R = rows; a.NH = n_heads;
   a.sl2 = scale * 1.4426950408889634f;
   const double flops = 4.0 * (double)rows * rows * 128.0 * n_heads;
@@ -1181,6 +1189,13 @@ int ming_attention(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int 
            "attention launch");
   c->eng.attention += 1;
   return ok();
+}
+
+int ming_attention(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int k_col,
+                   int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
+                   int head_dim, float scale) {
+  return attention_impl(c, qkv, ld, q_col, k_col, v_col, out, ldo, rows, n_heads, head_dim,
+                        scale, false);
 }
 
 
@@ -1462,6 +1477,13 @@ int rt_tanh_gates(ming_ctx* c, const uint16_t* mods, int n, float* t) {
            "tanh gates launch");
   c->eng.elementwise += 1;
   return ok();
+}
+
+int rt_attention_xh(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int k_col,
+                    int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
+                    float scale) {
+  return attention_impl(c, qkv, ld, q_col, k_col, v_col, out, ldo, rows, n_heads, 128, scale,
+                        true);
 }
 
 int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ldx,
