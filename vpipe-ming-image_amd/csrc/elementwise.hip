@@ -53,6 +53,33 @@ __global__ void tanh_gates_kernel(const uint16_t* mods, int n, float* t) {
   t[i] = tanhf(bf16_to_f32(mods[src]));
 }
 
+// A modulated block's adaLN glue in one pass over its n columns (fill_mod,
+// ming-dit.cc:2266-2273, with the gain fold): mods = bf16(mods + b) in
+// place, the two folded pre-norm gains nw1 = an1 * (1 + scale_msa) and
+// nw3 = fn1 * (1 + scale_mlp), and the two f32 residual gates
+// t = tanh(gate_msa | gate_mlp). Each value is the expression of
+// bias_act_kernel (mode 0), modulate_kernel and tanh_gates_kernel, so the
+// bits are theirs.
+__global__ void adaln_glue_kernel(uint16_t* mods, int n, const uint16_t* b,
+                                  const uint16_t* an1, const uint16_t* fn1, uint16_t* nw1,
+                                  uint16_t* nw3, float* t) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float m[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = q * n + i;
+    const float v = bf16_to_f32(mods[c]);
+    const uint16_t r = (uint16_t)f32_to_bf16_bits(v + bf16_to_f32(b[c]));
+    m[q] = bf16_to_f32(r);
+    mods[c] = (uint16_t)f32_to_bf16_bits(m[q]);
+  }
+  nw1[i] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(an1[i]) * (1.0f + m[0]) + 0.0f);
+  nw3[i] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(fn1[i]) * (1.0f + m[2]) + 0.0f);
+  t[i] = tanhf(m[1]);
+  t[n + i] = tanhf(m[3]);
+}
+
 // mode 0: h += tanh(gate[n]) * sub ; mode 1: h += sub
 __global__ void residual_kernel(uint16_t* h, long long ldh, const uint16_t* gate,
                                 const uint16_t* sub, long long lds, int rows,
@@ -222,6 +249,15 @@ hipError_t launch_swiglu(const uint16_t* g, long long ldg, const uint16_t* u,
   return hipGetLastError();
 }
 
+hipError_t launch_adaln_glue(uint16_t* mods, int n, const uint16_t* b, const uint16_t* an1,
+                             const uint16_t* fn1, uint16_t* nw1, uint16_t* nw3, float* t,
+                             hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(adaln_glue_kernel, dim3((n + 255) / 256), dim3(256), 0, s, mods, n, b, an1,
+                     fn1, nw1, nw3, t);
+  return hipGetLastError();
+}
+
 hipError_t launch_tanh_gates(const uint16_t* mods, int n, float* t, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(tanh_gates_kernel, dim3((2 * n + 255) / 256), dim3(256), 0, s, mods, n, t);
@@ -273,7 +309,8 @@ hipError_t launch_quantize(const float* w, int N, int K, int bits,
 
 hipError_t validate_elementwise_kernels() {
   hipFuncAttributes fa;
-  const void* fns[] = {reinterpret_cast<const void*>(&swiglu_kernel),
+  const void* fns[] = {reinterpret_cast<const void*>(&adaln_glue_kernel),
+                       reinterpret_cast<const void*>(&swiglu_kernel),
                        reinterpret_cast<const void*>(&residual_kernel),
                        reinterpret_cast<const void*>(&modulate_kernel),
                        reinterpret_cast<const void*>(&bias_act_kernel),

@@ -125,6 +125,11 @@ hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const u
 // t[i] = tanhf(bf16 g[i]) for the two gates of a block's adaLN output:
 // g = mods + n (gate_msa) and mods + 3n (gate_mlp) -> t[0, n) and t[n, 2n)
 hipError_t launch_tanh_gates(const uint16_t* mods, int n, float* t, hipStream_t s);
+// mods[4n] = bf16(mods + b) in place; nw1 = bf16(an1 * (1 + mods[0, n))),
+// nw3 = bf16(fn1 * (1 + mods[2n, 3n))); t as launch_tanh_gates
+hipError_t launch_adaln_glue(uint16_t* mods, int n, const uint16_t* b, const uint16_t* an1,
+                             const uint16_t* fn1, uint16_t* nw1, uint16_t* nw3, float* t,
+                             hipStream_t s);
 hipError_t launch_rope_table(const int32_t* pt, const int32_t* ph,
                              const int32_t* pw, int n, int a0, int a1, int a2,
                              int head_dim, double theta, float* cos_t,

@@ -106,10 +106,8 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
   if (modulated) {
     // mods = ada(temb) + ada_b = (scale_msa | gate_msa | scale_mlp | gate_mlp)
     RC(ming_lin(c, b->ada, temb, d.adaln_dim, w.mods, 4 * H, 1, nullptr));
-    RC(ming_bias_act(c, w.mods, 4 * H, b->ada_b, 1, 4 * H, 0));
-    RC(ming_modulate(c, b->an1, H, w.mods, w.nw1, H, 1, H));
-    RC(ming_modulate(c, b->fn1, H, w.mods + 2 * H, w.nw3, H, 1, H));
-    RC(ming::rt_tanh_gates(c, w.mods, H, w.tg));
+    // + bias, the two gain folds and the tanh of the two gates, one launch
+    RC(ming::rt_adaln_glue(c, w.mods, H, b->ada_b, b->an1, b->fn1, w.nw1, w.nw3, w.tg));
     g1 = w.nw1;
     g3 = w.nw3;
   }

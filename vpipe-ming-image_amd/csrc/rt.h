@@ -58,4 +58,8 @@ int rt_norm_residual(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
 // t[0, n) = tanh(mods[n, 2n)), t[n, 2n) = tanh(mods[3n, 4n)) in f32: a block's
 // two residual gates, once per block instead of once per element.
 int rt_tanh_gates(ming_ctx* c, const uint16_t* mods, int n, float* t);
+// ming_bias_act (mode 0) on the block's adaLN output, the two ming_modulate
+// gain folds and rt_tanh_gates, in one launch (the same bits as those four)
+int rt_adaln_glue(ming_ctx* c, uint16_t* mods, int n, const uint16_t* b, const uint16_t* an1,
+                  const uint16_t* fn1, uint16_t* nw1, uint16_t* nw3, float* t);
 }  // namespace ming

@@ -1470,6 +1470,19 @@ int rt_norm_residual(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
                   "post-norm residual");
 }
 
+int rt_adaln_glue(ming_ctx* c, uint16_t* mods, int n, const uint16_t* b, const uint16_t* an1,
+                  const uint16_t* fn1, uint16_t* nw1, uint16_t* nw3, float* t) {
+  DeviceGuard g(c->device);
+  MING_HIP(profiled(c, kBModulate, 0.0, 2.0 * 8 * n + 2.0 * 4 * n + 4.0 * 2 * n,
+                    [&] {
+                      return ming::launch_adaln_glue(mods, n, b, an1, fn1, nw1, nw3, t,
+                                                     c->stream);
+                    }),
+           "adaLN glue launch");
+  c->eng.elementwise += 1;
+  return ok();
+}
+
 int rt_tanh_gates(ming_ctx* c, const uint16_t* mods, int n, float* t) {
   DeviceGuard g(c->device);
   MING_HIP(profiled(c, kBModulate, 0.0, 2.0 * 2 * n + 4.0 * 2 * n,
