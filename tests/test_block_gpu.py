@@ -213,28 +213,37 @@ def public_block(ctx, gp, x, rows, c, s, temb, scales, modulated):
     return xd, nrm, qkv, ob, ffg, g3, mods if modulated else None
 
 
+@pytest.mark.parametrize("route", ["auto", "general"])
 @pytest.mark.parametrize("modulated", [True, False])
-def test_block_forward_equals_the_public_calls(ctx, modulated):
+def test_block_forward_equals_the_public_calls(ctx, modulated, route):
     """The block driver's fusions (the norm writing the fp16 copy q, k, v and
     w1, w3 read; post-norm + residual in one pass) give the same bits as the
-    public entry points called one by one."""
+    public entry points called one by one, on either projection route."""
     import torch
     rows = 136
     ob, gp, desc = build_block(ctx, 900 + modulated, H, F, ADA, 4, modulated)
     x = bf16(randn(47, (rows, H)))
     temb = bf16(randn(49, (ADA,))) if modulated else None
     c, s = tables(rows)
-    got = run_gpu(ctx, desc, dims(), x, rows, c, s, temb, SCALES)
-    xd, nrm, qkv, obd, ffg, g3, mods = public_block(ctx, gp, x, rows, c, s, temb, SCALES,
-                                                    modulated)
-    # the feed-forward half, public calls
-    y = torch.empty((rows, H), dtype=torch.int16, device="cuda")
-    ctx.ffn(gp["w1"], gp["w3"], gp["w2"], nrm, y, rows, SCALES, h=ffg)
-    ctx.rmsnorm(y, gp["fn2"], y, rows, H)
-    if modulated:
-        ctx.gated_residual(xd, mods[:, 3 * H:], y, rows, H)
-    else:
-        ctx.residual_add(xd, y, rows, H)
-    ctx.synchronize()
+    ctx.set_route(route)
+    try:
+        ctx.reset_engagement()
+        got = run_gpu(ctx, desc, dims(), x, rows, c, s, temb, SCALES)
+        eng = ctx.engagement()
+        assert eng["qk_norm_rope"] == 1
+        assert (eng["gemm_fast"] > 0) == (route == "auto")
+        xd, nrm, qkv, obd, ffg, g3, mods = public_block(ctx, gp, x, rows, c, s, temb,
+                                                        SCALES, modulated)
+        # the feed-forward half, public calls
+        y = torch.empty((rows, H), dtype=torch.int16, device="cuda")
+        ctx.ffn(gp["w1"], gp["w3"], gp["w2"], nrm, y, rows, SCALES, h=ffg)
+        ctx.rmsnorm(y, gp["fn2"], y, rows, H)
+        if modulated:
+            ctx.gated_residual(xd, mods[:, 3 * H:], y, rows, H)
+        else:
+            ctx.residual_add(xd, y, rows, H)
+        ctx.synchronize()
+    finally:
+        ctx.set_route("auto")
     want = from_dev(xd)
     assert np.array_equal(got, want)

@@ -155,25 +155,31 @@ __global__ void rope_table_kernel(const int32_t* pt, const int32_t* ph,
 }
 
 // One 16-lane group per (row, head) of q or k; each lane owns 8 elements
-// (4 interleaved pairs) of the 128-wide head.
+// (4 interleaved pairs) of the 128-wide head. Block (x, row): heads 16x ..
+// 16x + 15 of the row's 2 * n_heads (q then k), rows strided by the grid's y
+// extent, so no index division. The
+// kernel is near the memory bound with a heavy VALU share, so both bf16
+// roundings of a pair take gfx950's v_cvt_pk_bf16_f32 (round to nearest
+// even: the bits of the bit-twiddled rounding for every non-NaN value), and
+// every load is issued before the reduction.
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     uint16_t* __restrict__ x, long long ld, int q_col, int k_col, int rows,
     int n_heads, const uint16_t* __restrict__ wq,
     const uint16_t* __restrict__ wk, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, float eps) {
   const int tid = threadIdx.x, lane = tid & 63;
-  const long long hr = (long long)blockIdx.x * 16 + (tid >> 4);
+  for (int row = (int)blockIdx.y; row < rows; row += (int)gridDim.y) {
+  const int hh0 = (int)blockIdx.x * 16 + (tid >> 4);
   const int sub = lane & 15;
-  const long long total = (long long)rows * 2 * n_heads;
-  const bool live = hr < total;
-  const long long hrc = live ? hr : 0;
-  const int row = (int)(hrc / (2 * n_heads));
-  const int hh = (int)(hrc % (2 * n_heads));
+  const bool live = hh0 < 2 * n_heads;
+  const int hh = live ? hh0 : 0;
   const bool isk = hh >= n_heads;
   const int head = isk ? hh - n_heads : hh;
-  uint16_t* p = x + (long long)row * ld + (isk ? k_col : q_col) + head * 128 +
-                8 * sub;
+  uint16_t* p = x + (long long)row * ld + (isk ? k_col : q_col) + head * 128 + 8 * sub;
   const uint4 v = *reinterpret_cast<const uint4*>(p);
+  const uint4 wv = *reinterpret_cast<const uint4*>((isk ? wk : wq) + 8 * sub);
+  const float4 cv = *reinterpret_cast<const float4*>(cos_t + (long long)row * 64 + 4 * sub);
+  const float4 sv = *reinterpret_cast<const float4*>(sin_t + (long long)row * 64 + 4 * sub);
   const uint32_t* u = &v.x;
   float ss = 0.0f;
 #pragma unroll
@@ -185,11 +191,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 #pragma unroll
   for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
   const float inv = 1.0f / sqrtf(ss * (1.0f / 128.0f) + eps);
-  if (!live) return;
-  const uint4 wv = *reinterpret_cast<const uint4*>((isk ? wk : wq) + 8 * sub);
   const uint32_t* wu = &wv.x;
-  const float4 cv = *reinterpret_cast<const float4*>(cos_t + (long long)row * 64 + 4 * sub);
-  const float4 sv = *reinterpret_cast<const float4*>(sin_t + (long long)row * 64 + 4 * sub);
   const float cs[4] = {cv.x, cv.y, cv.z, cv.w};
   const float sn[4] = {sv.x, sv.y, sv.z, sv.w};
   uint4 o;
@@ -197,16 +199,16 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     // the norm, rounded to bf16 as the reference stores it
-    const float a = bf16_to_f32((uint16_t)f32_to_bf16_bits(
-        __fmul_rn(__fmul_rn(bf16_lo(u[e]), inv), bf16_lo(wu[e]))));
-    const float b = bf16_to_f32((uint16_t)f32_to_bf16_bits(
-        __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv), bf16_hi(wu[e]))));
+    const uint32_t nb = pack_bf16x2_rne(__fmul_rn(__fmul_rn(bf16_lo(u[e]), inv), bf16_lo(wu[e])),
+                                        __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv), bf16_hi(wu[e])));
+    const float a = bf16_lo(nb), b = bf16_hi(nb);
     // (a + i b)(c + i s)
     const float re = __fsub_rn(__fmul_rn(a, cs[e]), __fmul_rn(b, sn[e]));
     const float im = __fadd_rn(__fmul_rn(a, sn[e]), __fmul_rn(b, cs[e]));
-    ou[e] = pack_bf16x2(re, im);
+    ou[e] = pack_bf16x2_rne(re, im);
   }
-  *reinterpret_cast<uint4*>(p) = o;
+  if (live) *reinterpret_cast<uint4*>(p) = o;
+  }
 }
 
 }  // namespace
@@ -265,9 +267,9 @@ hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
                                const uint16_t* wq, const uint16_t* wk,
                                const float* cos_t, const float* sin_t,
                                float eps, hipStream_t s) {
-  const long long total = (long long)rows * 2 * n_heads;
-  if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((total + 15) / 16)),
+  if (rows <= 0 || n_heads <= 0) return hipSuccess;
+  const unsigned gy = (unsigned)(rows < 65535 ? rows : 65535);   // grid y limit; rows stride
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((2 * n_heads + 15) / 16), gy),
                      dim3(256), 0, s, x, ld, q_col, k_col, rows, n_heads, wq,
                      wk, cos_t, sin_t, eps);
   return hipGetLastError();
