@@ -32,7 +32,9 @@ namespace {
 // MODE 3: h = bf16(h + y): the same for the context refiner's plain residual.
 // Every mode reduces a row exactly as MODE 0 does and rounds y to bf16 before
 // the residual, so each is bit-identical to rmsnorm followed by the separate
-// residual / conversion kernel.
+// residual / conversion kernel. Roundings to bf16 take v_cvt_pk_bf16_f32
+// (round to nearest even; the bit-twiddled rounding's bits for every
+// non-NaN value), two VALU per pair fewer than the bit arithmetic.
 template <int LPR, int CPL, int MODE>
 __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
     const uint16_t* x, long long ldx, const uint16_t* __restrict__ w,
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
       for (int e = 0; e < 4; ++e) {
         const float a = __fmul_rn(__fmul_rn(bf16_lo(u[e]), inv), bf16_lo(wu[e]));
         const float b = __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv), bf16_hi(wu[e]));
-        ou[e] = pack_bf16x2(a, b);
+        ou[e] = pack_bf16x2_rne(a, b);
       }
       if (MODE <= 1) {
         *reinterpret_cast<uint4*>(y + (long long)row * ldy + 8 * c) = o;
@@ -120,7 +122,7 @@ __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
             s0 = __fmul_rn(t[2 * e], s0);
             s1 = __fmul_rn(t[2 * e + 1], s1);
           }
-          rp[e] = pack_bf16x2(__fadd_rn(bf16_lo(hp[e]), s0), __fadd_rn(bf16_hi(hp[e]), s1));
+          rp[e] = pack_bf16x2_rne(__fadd_rn(bf16_lo(hp[e]), s0), __fadd_rn(bf16_hi(hp[e]), s1));
         }
         *reinterpret_cast<uint4*>(h + (long long)row * ldh + 8 * c) = r;
       }

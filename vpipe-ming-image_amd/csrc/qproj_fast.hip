@@ -877,13 +877,18 @@ hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s) {
 // The K split depends on M and K only, never on how many columns are
 // stacked: each T column is then summed in the same order, and so has the
 // same bits, whether its projection's x.A runs alone or stacked with others
-// over the same x. It is sized as if a launch held 5 column blocks (between
-// one projection's 2.5 and q|k|v's 7.5 at the config-2 adapter set): at 4352
-// rows that is 3 slices, measured best of 1, 2, 3, 5 and 8 over the
-// 1024^2 forward's 136 launches (6.59 ms against 6.91 ms for 5).
+// over the same x. It is sized for an assumed number of 128-wide column
+// blocks per launch, by K:
+//  - K <= 4096 (the hidden-width inputs: q|k|v, o, w1|w3): 5 blocks, between
+//    one projection's 2.5 and q|k|v's 7.5 at the config-2 adapter set. At
+//    4352 rows that is 3 slices, measured best of 1, 2, 3, 5 and 8 over the
+//    1024^2 forward's 136 launches (6.59 ms against 6.91 ms for 5).
+//  - K > 4096 (the FFN-width input of w2, whose x.A always runs alone): 3
+//    blocks, i.e. 5 slices at 4352 rows, one round of 255 blocks (forward
+//    65.18 ms against 65.57 ms for 3 slices and 65.57 ms for 8).
 int lora_xa_fast_slices(int M, int n_cols, int K) {
   (void)n_cols;
-  const int tiles = ((M + 255) / 256) * 5;
+  const int tiles = ((M + 255) / 256) * (K > 4096 ? 3 : 5);
   const int KT = K / 64;
   int ks = 256 / (tiles > 0 ? tiles : 1);       // about one round of the chip
   const int kmax = KT / 8 > 1 ? KT / 8 : 1;      // keep >= 8 K steps per slice
