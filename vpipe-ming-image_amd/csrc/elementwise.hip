@@ -37,8 +37,8 @@ __global__ void swiglu_kernel(const uint16_t* g, long long ldg,
     uint32_t* op = &o.x;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      op[e] = pack_bf16x2(silu_f(bf16_lo(gp[e])) * bf16_lo(up[e]),
-                          silu_f(bf16_hi(gp[e])) * bf16_hi(up[e]));
+      op[e] = pack_bf16x2_rne(silu_f(bf16_lo(gp[e])) * bf16_lo(up[e]),
+                              silu_f(bf16_hi(gp[e])) * bf16_hi(up[e]));
     *reinterpret_cast<uint4*>(out + r * ldo + c) = o;
   }
 }

@@ -306,8 +306,8 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
         const int n = n0 + 128 * wn + 32 * j + 8 * q + 4 * fk;
         if (m < a.M && n < a.N) {
           uint2 v;
-          v.x = pack_bf16x2(acc[j][i][4 * q + 0], acc[j][i][4 * q + 1]);
-          v.y = pack_bf16x2(acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
+          v.x = pack_bf16x2_rne(acc[j][i][4 * q + 0], acc[j][i][4 * q + 1]);
+          v.y = pack_bf16x2_rne(acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
           *reinterpret_cast<uint2*>(a.y + (long long)m * a.ldy + n) = v;
         }
       }
@@ -397,8 +397,8 @@ __global__ __launch_bounds__(256, 2) void lora_xa_kernel(const LoraXaArgs a) {
       const int c = c0 + 32 * j + 8 * q + 4 * fk;
       const float f = a.coef[c >> 4];
       uint2 v;
-      v.x = pack_bf16x2(f * acc[j][4 * q + 0], f * acc[j][4 * q + 1]);
-      v.y = pack_bf16x2(f * acc[j][4 * q + 2], f * acc[j][4 * q + 3]);
+      v.x = pack_bf16x2_rne(f * acc[j][4 * q + 0], f * acc[j][4 * q + 1]);
+      v.y = pack_bf16x2_rne(f * acc[j][4 * q + 2], f * acc[j][4 * q + 3]);
       *reinterpret_cast<uint2*>(a.t + (long long)m * a.ldt + c) = v;
     }
   }

@@ -543,8 +543,8 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
           uint32_t* vp = &v.x;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            vp[e] = pack_bf16x2(silu_f(bf16_lo(gp[e])) * bf16_lo(vp[e]),
-                                silu_f(bf16_hi(gp[e])) * bf16_hi(vp[e]));
+            vp[e] = pack_bf16x2_rne(silu_f(bf16_lo(gp[e])) * bf16_lo(vp[e]),
+                                    silu_f(bf16_hi(gp[e])) * bf16_hi(vp[e]));
         }
         uint16_t* yp = a.y + (long long)m * a.ldy + n;
         if (st16) {
@@ -744,8 +744,8 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
           if (f == 0.0f) {
             v = make_uint2(0, 0);
           } else {
-            v.x = pack_bf16x2(f * acc[i][j][4 * q + 0], f * acc[i][j][4 * q + 1]);
-            v.y = pack_bf16x2(f * acc[i][j][4 * q + 2], f * acc[i][j][4 * q + 3]);
+            v.x = pack_bf16x2_rne(f * acc[i][j][4 * q + 0], f * acc[i][j][4 * q + 1]);
+            v.y = pack_bf16x2_rne(f * acc[i][j][4 * q + 2], f * acc[i][j][4 * q + 3]);
           }
           *reinterpret_cast<uint2*>(a.t + (long long)m * a.ldt + c) = v;
         } else {
@@ -779,8 +779,8 @@ __global__ void lora_xa_reduce_kernel(const float* part, int kslices, int M,
     if (f == 0.0f) {
       o = make_uint2(0, 0);
     } else {
-      o.x = pack_bf16x2(f * s.x, f * s.y);
-      o.y = pack_bf16x2(f * s.z, f * s.w);
+      o.x = pack_bf16x2_rne(f * s.x, f * s.y);
+      o.y = pack_bf16x2_rne(f * s.z, f * s.w);
     }
     *reinterpret_cast<uint2*>(a.t + m * a.ldt + c) = o;
   }
