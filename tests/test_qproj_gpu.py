@@ -340,3 +340,28 @@ def test_ffn_rejects_mismatched_shapes(ctx):
     y = empty_bf16(M, H)
     with pytest.raises(m.MingError):
         ctx.ffn(w1, w2, w2, x, y, M)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 3840, 2560), (4096, 64, 3840), (200, 192, 1024)])
+def test_dense_few_tiles_parity(ctx, orc, M, N, K):
+    """Dense weights whose output is a few 256 x 256 tiles (the caption
+    embedder, the final layer) take the split-K GEMM on the auto route: to
+    the bar against the fp32 reference, with row strides, writing only the
+    M x N block (the route fixture runs the general kernel on it as well)."""
+    print(f"case dense M={M} N={N} K={K}", flush=True)
+    x = bf16(randn(700 + M, (M, K + 64)))
+    pack, w = make_weight(701 + N, N, K, 16)
+    qw = _qw(ctx, pack, 16)
+    ldy = N + 36
+    y = to_dev(np.full((M, ldy), 0x2345, np.uint16))
+    sync()
+    ctx.reset_engagement()
+    ctx.lin(qw, to_dev(x), y, M, ldx=K + 64, ldy=ldy)
+    sync()
+    eng = ctx.engagement()
+    assert eng["gemm_dense"] == 1 and eng["gemm_fast"] == 0 and eng["gemv"] == 0
+    out = from_dev(y)
+    assert (out[:, N:] == 0x2345).all()
+    ref = orc.proj(np.ascontiguousarray(x[:, :K]), w)
+    assert _rel(orc, np.ascontiguousarray(out[:, :N]), ref) <= TOL
+    qw.close()

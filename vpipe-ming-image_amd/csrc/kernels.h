@@ -188,6 +188,9 @@ hipError_t launch_repack_fast(int bits, const uint32_t* codes,
 // x.A_live^T with split-K: `part` holds kslices * M * n_cols f32 (unused
 // when kslices == 1).
 int lora_xa_fast_slices(int M, int n_cols, int K);
+// The same kernel as a plain split-K bf16 GEMM y = x . W^T of a dense W
+// [N][K] (identity groups, coefficient 1): its slice count.
+int dense_xa_slices(int M, int N, int K);
 hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s);
 hipError_t launch_bf16_to_f16(const uint16_t* x, long long ldx, uint16_t* y,

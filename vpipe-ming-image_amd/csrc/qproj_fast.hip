@@ -896,6 +896,17 @@ int lora_xa_fast_slices(int M, int n_cols, int K) {
   return ks < 1 ? 1 : ks;
 }
 
+// A dense projection through the x.A kernel: as many slices as fill about
+// one round of the chip, at least 8 K steps each.
+int dense_xa_slices(int M, int N, int K) {
+  const int tiles = ((M + 255) / 256) * ((N + 127) / 128);
+  const int KT = K / 64;
+  int ks = 256 / (tiles > 0 ? tiles : 1);
+  const int kmax = KT / 8 > 1 ? KT / 8 : 1;
+  if (ks > kmax) ks = kmax;
+  return ks < 1 ? 1 : ks;
+}
+
 hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s) {
   if (a.M <= 0 || a.n_cols <= 0) return hipSuccess;

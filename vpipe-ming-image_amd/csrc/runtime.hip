@@ -964,13 +964,42 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
                               : (double)q->N * K * q->bits / 8 + 4.0 * q->N * (K / 64);
     const int bk = fast[i] ? (q->bits == 4 ? kBF4 : kBF8)
                            : (q->bits == 4 ? kBQ4 : (q->bits == 8 ? kBQ8 : kBDense));
-    MING_HIP(profiled(c, bk, base_flops + tail_flops[i],
-                      2.0 * M * K + wbytes + 2.0 * M * q->N,
-                      [&] {
-                        return fast[i] ? ming::launch_qproj_fast(q->bits, a, c->stream)
-                                       : ming::launch_qproj(q->bits, a, c->stream);
-                      }),
-             "qproj launch");
+    // A dense weight with no live adapter whose output is a few 256 x 256
+    // tiles (the caption embedder at 256 rows: 15 tiles; the final layer's 64
+    // columns: 16) runs as the x.A path's split-K bf16 GEMM -- identity
+    // column groups, coefficient 1 -- which spreads K over the chip.
+    const bool dense_sk =
+        q->bits == 16 && c->route == MING_ROUTE_AUTO && live_segs[i] == 0 && !o.gate &&
+        !o.yh && ((M + 255) / 256) * ((q->N + 255) / 256) < 64 && q->N % 64 == 0 &&
+        q->N <= 16 * ming::kMaxGroups && K % 64 == 0 && o.ldy <= (1 << 30) &&
+        (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) &&
+        (uint64_t)q->N * (uint64_t)K * 2 <= (1ull << 32);
+    if (dense_sk) {
+      const int dks = ming::dense_xa_slices(M, q->N, K);
+      if (dks > 1) {
+        int rc = ensure_part(c, (size_t)dks * M * q->N * 4);
+        if (rc != MING_OK) return rc;
+      }
+      ming::LoraXaArgs da{};
+      da.x = x; da.ldx = ldx; da.A[0] = q->w16; da.K = K; da.M = M;
+      da.n_cols = q->N; da.t = o.y; da.ldt = (int)o.ldy;
+      for (int g = 0; g < q->N / 16; ++g) {
+        da.grp[g] = (int16_t)g;
+        da.coef[g] = 1.0f;
+      }
+      MING_HIP(profiled(c, bk, base_flops, 2.0 * M * K + wbytes + 2.0 * M * q->N,
+                        [&] { return ming::launch_lora_xa_fast(da, (float*)c->part, dks,
+                                                               c->stream); }),
+               "dense split-K launch");
+    } else {
+      MING_HIP(profiled(c, bk, base_flops + tail_flops[i],
+                        2.0 * M * K + wbytes + 2.0 * M * q->N,
+                        [&] {
+                          return fast[i] ? ming::launch_qproj_fast(q->bits, a, c->stream)
+                                         : ming::launch_qproj(q->bits, a, c->stream);
+                        }),
+               "qproj launch");
+    }
     if (o.gate && !fast[i]) {
       // the general route writes the projection; SwiGLU follows
       MING_HIP(profiled(c, kBSwiglu, 0.0, 6.0 * M * q->N,
