@@ -60,9 +60,9 @@ __global__ void tanh_gates_kernel(const uint16_t* mods, int n, float* t) {
 // t = tanh(gate_msa | gate_mlp). Each value is the expression of
 // bias_act_kernel (mode 0), modulate_kernel and tanh_gates_kernel, so the
 // bits are theirs.
-__global__ void adaln_glue_kernel(uint16_t* mods, int n, const uint16_t* b,
-                                  const uint16_t* an1, const uint16_t* fn1, uint16_t* nw1,
-                                  uint16_t* nw3, float* t) {
+__device__ __forceinline__ void adaln_glue_body(uint16_t* mods, int n, const uint16_t* b,
+                                                const uint16_t* an1, const uint16_t* fn1,
+                                                uint16_t* nw1, uint16_t* nw3, float* t) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float m[4];
@@ -78,6 +78,17 @@ __global__ void adaln_glue_kernel(uint16_t* mods, int n, const uint16_t* b,
   nw3[i] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(fn1[i]) * (1.0f + m[2]) + 0.0f);
   t[i] = tanhf(m[1]);
   t[n + i] = tanhf(m[3]);
+}
+
+__global__ void adaln_glue_kernel(uint16_t* mods, int n, const uint16_t* b,
+                                  const uint16_t* an1, const uint16_t* fn1, uint16_t* nw1,
+                                  uint16_t* nw3, float* t) {
+  adaln_glue_body(mods, n, b, an1, fn1, nw1, nw3, t);
+}
+
+__global__ void adaln_glue_batch_kernel(const GlueBatch g) {
+  const GlueEntry& e = g.e[blockIdx.y];
+  adaln_glue_body(e.mods, g.n, e.b, e.an1, e.fn1, e.nw1, e.nw3, e.t);
 }
 
 // mode 0: h += tanh(gate[n]) * sub ; mode 1: h += sub
@@ -258,6 +269,14 @@ hipError_t launch_adaln_glue(uint16_t* mods, int n, const uint16_t* b, const uin
   return hipGetLastError();
 }
 
+hipError_t launch_adaln_glue_batch(const GlueBatch& g, hipStream_t s) {
+  if (g.n <= 0 || g.count <= 0) return hipSuccess;
+  if (g.count > 32) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(adaln_glue_batch_kernel, dim3((g.n + 255) / 256, g.count), dim3(256), 0, s,
+                     g);
+  return hipGetLastError();
+}
+
 hipError_t launch_tanh_gates(const uint16_t* mods, int n, float* t, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(tanh_gates_kernel, dim3((2 * n + 255) / 256), dim3(256), 0, s, mods, n, t);
@@ -310,6 +329,7 @@ hipError_t launch_quantize(const float* w, int N, int K, int bits,
 hipError_t validate_elementwise_kernels() {
   hipFuncAttributes fa;
   const void* fns[] = {reinterpret_cast<const void*>(&adaln_glue_kernel),
+                       reinterpret_cast<const void*>(&adaln_glue_batch_kernel),
                        reinterpret_cast<const void*>(&swiglu_kernel),
                        reinterpret_cast<const void*>(&residual_kernel),
                        reinterpret_cast<const void*>(&modulate_kernel),

@@ -72,7 +72,7 @@ __device__ __forceinline__ void load_group(const GemvArgs& a, int n, int kt, flo
 }
 
 template <int BITS>
-__global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
+__device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   __shared__ float red[4][kGemvMaxM][64];
   const int lane = (int)threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -127,7 +127,37 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   }
 }
 
+template <int BITS>
+__global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
+  gemv_body<BITS>(a);
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void gemv_batch_kernel(const GemvBatch b) {
+  GemvArgs a = b.base;
+  const GemvEntry& e = b.e[blockIdx.y];
+  a.codes = e.codes;
+  a.sb = e.sb;
+  a.w16 = e.w16;
+  a.y = e.y;
+  gemv_body<BITS>(a);
+}
+
 }  // namespace
+
+hipError_t launch_gemv_batch(int bits, const GemvBatch& b, hipStream_t s) {
+  const GemvArgs& a = b.base;
+  if (b.count <= 0 || a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (b.count > kGemvBatch || a.M > kGemvMaxM || a.K % 64 != 0) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)b.count);
+  switch (bits) {
+    case 4: hipLaunchKernelGGL(gemv_batch_kernel<4>, grid, dim3(256), 0, s, b); break;
+    case 8: hipLaunchKernelGGL(gemv_batch_kernel<8>, grid, dim3(256), 0, s, b); break;
+    case 16: hipLaunchKernelGGL(gemv_batch_kernel<16>, grid, dim3(256), 0, s, b); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_gemv(int bits, const GemvArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
@@ -146,7 +176,10 @@ hipError_t validate_gemv_kernels() {
   hipFuncAttributes fa;
   const void* fns[] = {reinterpret_cast<const void*>(&gemv_kernel<4>),
                        reinterpret_cast<const void*>(&gemv_kernel<8>),
-                       reinterpret_cast<const void*>(&gemv_kernel<16>)};
+                       reinterpret_cast<const void*>(&gemv_kernel<16>),
+                       reinterpret_cast<const void*>(&gemv_batch_kernel<4>),
+                       reinterpret_cast<const void*>(&gemv_batch_kernel<8>),
+                       reinterpret_cast<const void*>(&gemv_batch_kernel<16>)};
   for (const void* f : fns) {
     const hipError_t e = hipFuncGetAttributes(&fa, f);
     if (e != hipSuccess) return e;

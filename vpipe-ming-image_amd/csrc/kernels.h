@@ -127,6 +127,22 @@ hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const u
 hipError_t launch_tanh_gates(const uint16_t* mods, int n, float* t, hipStream_t s);
 // mods[4n] = bf16(mods + b) in place; nw1 = bf16(an1 * (1 + mods[0, n))),
 // nw3 = bf16(fn1 * (1 + mods[2n, 3n))); t as launch_tanh_gates
+// launch_adaln_glue over up to kGemvBatch blocks in one launch (grid y = entry).
+struct GlueEntry {
+  uint16_t* mods;
+  const uint16_t* b;
+  const uint16_t* an1;
+  const uint16_t* fn1;
+  uint16_t* nw1;
+  uint16_t* nw3;
+  float* t;
+};
+struct GlueBatch {
+  int n;
+  int count;
+  GlueEntry e[32];
+};
+hipError_t launch_adaln_glue_batch(const GlueBatch& b, hipStream_t s);
 hipError_t launch_adaln_glue(uint16_t* mods, int n, const uint16_t* b, const uint16_t* an1,
                              const uint16_t* fn1, uint16_t* nw1, uint16_t* nw3, float* t,
                              hipStream_t s);
@@ -176,6 +192,22 @@ struct GemvArgs {
   int M, N, K;
 };
 hipError_t launch_gemv(int bits, const GemvArgs& a, hipStream_t s);
+// Up to kGemvBatch GEMVs of one shape over one x in one launch (grid y =
+// entry): the per-block adaLN projections of a forward, each entry's bits
+// those of launch_gemv on it.
+constexpr int kGemvBatch = 32;
+struct GemvEntry {
+  const uint32_t* codes;
+  const uint32_t* sb;
+  const uint16_t* w16;
+  uint16_t* y;
+};
+struct GemvBatch {
+  GemvArgs base;       // x, ldx, ldy, M, N, K (the entry pointers unused)
+  int count;
+  GemvEntry e[kGemvBatch];
+};
+hipError_t launch_gemv_batch(int bits, const GemvBatch& b, hipStream_t s);
 hipError_t validate_gemv_kernels();
 
 // ---- the fast quantized route (qproj_fast.hip) --------------------------------

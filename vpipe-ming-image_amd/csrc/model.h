@@ -22,6 +22,7 @@ struct ming_model {
            *temb = nullptr, *tsilu = nullptr, *outmod = nullptr;
   float *cos_t = nullptr, *sin_t = nullptr;
   int32_t* pos = nullptr;
+  void* premod = nullptr;   // every modulated block's adaLN results, made per forward
   void* blk_ws = nullptr;
   size_t blk_bytes = 0;
   std::vector<uint16_t> tin_host;

@@ -94,22 +94,37 @@ int check_block(const ming_block_desc* b, const ming_block_dims& d, bool modulat
   return MING_OK;
 }
 
-// run_block (ming-dit.cc:2065-2263) with fill_mod folded in.
+// A modulated block's adaLN results, made ahead of the block.
+struct Premod {
+  uint16_t *mods, *nw1, *nw3;
+  float* tg;
+};
+
+// run_block (ming-dit.cc:2065-2263) with fill_mod folded in; pm: the
+// block's modulation already computed (rt_modulation_batch), else it is
+// computed here.
 int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& d,
                   uint16_t* x, int rows, const float* cos_t, const float* sin_t,
-                  const uint16_t* temb, const float* scales, const BlockWs& w) {
+                  const uint16_t* temb, const float* scales, const BlockWs& w,
+                  const Premod* pm = nullptr) {
   const int H = d.hidden, F = d.ffn, NH = d.n_heads;
   const bool modulated = b->ada != nullptr;
   const float eps = d.eps;
   const uint16_t* g1 = b->an1;
   const uint16_t* g3 = b->fn1;
-  if (modulated) {
+  const float* tg = nullptr;
+  if (modulated && pm) {
+    g1 = pm->nw1;
+    g3 = pm->nw3;
+    tg = pm->tg;
+  } else if (modulated) {
     // mods = ada(temb) + ada_b = (scale_msa | gate_msa | scale_mlp | gate_mlp)
     RC(ming_lin(c, b->ada, temb, d.adaln_dim, w.mods, 4 * H, 1, nullptr));
     // + bias, the two gain folds and the tanh of the two gates, one launch
     RC(ming::rt_adaln_glue(c, w.mods, H, b->ada_b, b->an1, b->fn1, w.nw1, w.nw3, w.tg));
     g1 = w.nw1;
     g3 = w.nw3;
+    tg = w.tg;
   }
   // ---- attention half ----
   // the norm also writes the fp16 copy q, k and v read (one conversion, not three)
@@ -127,13 +142,11 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
                            1.0f / std::sqrt(128.0f)));
   RC(ming::rt_lin_xh(c, b->o, w.nrm, H, w.ob, H, rows, scales));
   // post-norm and the (gated) residual in one pass
-  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->an2, modulated ? w.tg : nullptr, rows, H,
-                            eps));
+  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->an2, tg, rows, H, eps));
   // ---- feed-forward half (gpu_ff, 2151-2162; SwiGLU fused into w3) ----
   RC(ming::rt_rmsnorm_f16(c, x, H, g3, w.nrm, H, rows, H, eps));
   RC(ming::rt_ffn_xh(c, b->w1, b->w3, b->w2, w.nrm, H, w.ob, H, rows, scales, w.ffg, F));
-  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->fn2, modulated ? w.tg + H : nullptr, rows,
-                            H, eps));
+  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->fn2, tg ? tg + H : nullptr, rows, H, eps));
   return MING_OK;
 }
 
@@ -151,16 +164,34 @@ uint16_t host_bf16(float f) {
 
 namespace {
 
+// A modulated block's adaLN results: mods [4H], nw1 [H], nw3 [H] (bf16), tg
+// [2H] (f32), each 256-byte aligned.
+size_t premod_bytes(size_t H) {
+  return align256(8 * H) + 2 * align256(2 * H) + align256(8 * H);
+}
+
+Premod premod_of(void* base, size_t H, int i) {
+  char* p = static_cast<char*>(base) + (size_t)i * premod_bytes(H);
+  Premod r;
+  r.mods = reinterpret_cast<uint16_t*>(p);
+  r.nw1 = reinterpret_cast<uint16_t*>(p + align256(8 * H));
+  r.nw3 = reinterpret_cast<uint16_t*>(p + align256(8 * H) + align256(2 * H));
+  r.tg = reinterpret_cast<float*>(p + align256(8 * H) + 2 * align256(2 * H));
+  return r;
+}
+
 // One allocation for every per-forward plane of a joint length JT and Q query rows.
 int ensure_model_ws(ming_model* m, int JT, int Q) {
   if (JT <= m->ws_rows && Q <= m->ws_q) return MING_OK;
   const ming_model_desc& d = m->d;
   const size_t H = (size_t)d.hidden;
-  const size_t sz[10] = {(size_t)JT * H * 2,         (size_t)std::max(Q, 1) * d.cap_dim * 2,
+  const size_t NM = (size_t)(d.n_refiner + d.n_layers);
+  const size_t sz[11] = {(size_t)JT * H * 2,         (size_t)std::max(Q, 1) * d.cap_dim * 2,
                          (size_t)d.time_freq * 2,    (size_t)d.time_mid * 2,
                          (size_t)d.adaln_dim * 2,    (size_t)d.adaln_dim * 2,
                          H * 2,                      (size_t)JT * 64 * 4,
-                         (size_t)JT * 64 * 4,        (size_t)JT * 3 * 4};
+                         (size_t)JT * 64 * 4,        (size_t)JT * 3 * 4,
+                         NM * premod_bytes(H)};
   size_t total = 0;
   for (size_t s : sz) total += align256(s);
   ming_block_dims bd{d.hidden, d.n_heads, d.ffn, d.adaln_dim, d.eps};
@@ -174,10 +205,11 @@ int ensure_model_ws(ming_model* m, int JT, int Q) {
     return rt_fail(MING_ERR_ALLOC, "ming_model_forward: workspace allocation failed");
   m->ws_bytes = total + blk;
   char* p = static_cast<char*>(m->ws);
-  void** dst[10] = {(void**)&m->joint, (void**)&m->capn, (void**)&m->tin,   (void**)&m->te1,
+  void** dst[11] = {(void**)&m->joint, (void**)&m->capn, (void**)&m->tin,   (void**)&m->te1,
                     (void**)&m->temb,  (void**)&m->tsilu, (void**)&m->outmod,
-                    (void**)&m->cos_t, (void**)&m->sin_t, (void**)&m->pos};
-  for (int i = 0; i < 10; ++i) {
+                    (void**)&m->cos_t, (void**)&m->sin_t, (void**)&m->pos,
+                    (void**)&m->premod};
+  for (int i = 0; i < 11; ++i) {
     *dst[i] = p;
     p += align256(sz[i]);
   }
@@ -631,12 +663,34 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
         hipMemcpyAsync(fill->key, cap, cap_bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
       return rt_fail(MING_ERR_HIP, "ming_model_forward: caption cache fill failed");
   }
+  // every modulated block's adaLN modulation depends on temb alone: one
+  // batched GEMV + glue for all of them instead of two launches per block
+  bool premod = false;
+  {
+    std::vector<const ming_qweight*> ada(NM);
+    std::vector<const uint16_t*> ada_b(NM), an1(NM), fn1(NM);
+    std::vector<uint16_t*> mods(NM), nw1(NM), nw3(NM);
+    std::vector<float*> tg(NM);
+    bool all = true;
+    for (int L = 0; L < NM; ++L) {
+      const ming_block_desc& b = m->blocks[(size_t)L];
+      if (!b.ada) all = false;
+      const Premod p = premod_of(m->premod, (size_t)H, L);
+      ada[L] = b.ada; ada_b[L] = b.ada_b; an1[L] = b.an1; fn1[L] = b.fn1;
+      mods[L] = p.mods; nw1[L] = p.nw1; nw3[L] = p.nw3; tg[L] = p.tg;
+    }
+    if (all)
+      RC(ming::rt_modulation_batch(c, NM, ada.data(), ada_b.data(), an1.data(), fn1.data(),
+                                   m->temb, H, mods.data(), nw1.data(), nw3.data(), tg.data(),
+                                   nullptr, &premod));
+  }
   for (int L = 0; L < NM; ++L) {
     if (stop_requested(m)) return stopped(s);
     prog.poll(false);
     const int rows = L < d.n_refiner ? IMG : JT;
+    const Premod pm = premod_of(m->premod, (size_t)H, L);
     RC(block_forward(c, &m->blocks[(size_t)L], bd, m->joint, rows, m->cos_t, m->sin_t,
-                     m->temb, m->scales, w));
+                     m->temb, m->scales, w, premod ? &pm : nullptr));
     RC(prog.done_block(s));
     // with a stop wired, the host stays within 4 blocks of the GPU so that a
     // stop requested mid-forward is seen (ming-dit.cc:2530-2540)

@@ -62,4 +62,15 @@ int rt_tanh_gates(ming_ctx* c, const uint16_t* mods, int n, float* t);
 // gain folds and rt_tanh_gates, in one launch (the same bits as those four)
 int rt_adaln_glue(ming_ctx* c, uint16_t* mods, int n, const uint16_t* b, const uint16_t* an1,
                   const uint16_t* fn1, uint16_t* nw1, uint16_t* nw3, float* t);
+// Every modulated block's adaLN modulation of a forward at once (it depends
+// on temb alone): mods[i] = ada[i](temb) + ada_b[i] and the glue of
+// rt_adaln_glue, as one batched GEMV and one batched glue launch per 32
+// blocks, each block's bits those of ming_lin + rt_adaln_glue. *done is
+// false (nothing launched) when the per-block projections would not run the
+// GEMV: another route, a live adapter on an adaLN weight, mixed shapes.
+int rt_modulation_batch(ming_ctx* c, int count, const ming_qweight* const* ada,
+                        const uint16_t* const* ada_b, const uint16_t* const* an1,
+                        const uint16_t* const* fn1, const uint16_t* temb, int H,
+                        uint16_t* const* mods, uint16_t* const* nw1, uint16_t* const* nw3,
+                        float* const* tg, const float* scales, bool* done);
 }  // namespace ming

@@ -1512,6 +1512,62 @@ int rt_adaln_glue(ming_ctx* c, uint16_t* mods, int n, const uint16_t* b, const u
   return ok();
 }
 
+int rt_modulation_batch(ming_ctx* c, int count, const ming_qweight* const* ada,
+                        const uint16_t* const* ada_b, const uint16_t* const* an1,
+                        const uint16_t* const* fn1, const uint16_t* temb, int H,
+                        uint16_t* const* mods, uint16_t* const* nw1, uint16_t* const* nw3,
+                        float* const* tg, const float* scales, bool* done) {
+  *done = false;
+  if (count <= 0 || c->route != MING_ROUTE_AUTO || !ada[0]) return ok();
+  const ming_qweight* q0 = ada[0];
+  for (int i = 0; i < count; ++i) {
+    const ming_qweight* q = ada[i];
+    if (!q || q->ctx != c || q->bits != q0->bits || q->N != 4 * H || q->K != q0->K ||
+        q->K % 64 != 0)
+      return ok();
+    // the per-block projection runs the GEMV only with no live adapter
+    for (const Segment& sg : q->segs)
+      for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl)
+        if (sg.slot[sl].rank > 0 && scales && scales[sl] != 0.0f) return ok();
+  }
+  DeviceGuard g(c->device);
+  const double wbytes = q0->bits == 16 ? 2.0 * q0->N * q0->K
+                                       : (double)q0->N * q0->K * q0->bits / 8 +
+                                             4.0 * q0->N * (q0->K / 64);
+  for (int b0 = 0; b0 < count; b0 += ming::kGemvBatch) {
+    const int nb = std::min(ming::kGemvBatch, count - b0);
+    ming::GemvBatch gb{};
+    gb.base.x = temb; gb.base.ldx = q0->K; gb.base.ldy = q0->N;
+    gb.base.M = 1; gb.base.N = q0->N; gb.base.K = q0->K;
+    gb.count = nb;
+    ming::GlueBatch gl{};
+    gl.n = H;
+    gl.count = nb;
+    for (int j = 0; j < nb; ++j) {
+      const ming_qweight* q = ada[b0 + j];
+      gb.e[j] = {q->codes_t, q->sb, q->w16, mods[b0 + j]};
+      gl.e[j] = {mods[b0 + j], ada_b[b0 + j], an1[b0 + j], fn1[b0 + j],
+                 nw1[b0 + j],  nw3[b0 + j],   tg[b0 + j]};
+    }
+    MING_HIP(profiled(c, kBGemv, 2.0 * nb * q0->N * (double)q0->K,
+                      nb * (wbytes + 2.0 * q0->K + 2.0 * q0->N),
+                      [&] { return ming::launch_gemv_batch(q0->bits, gb, c->stream); }),
+             "batched gemv launch");
+    MING_HIP(profiled(c, kBModulate, 0.0, nb * (2.0 * 8 * H + 2.0 * 4 * H + 4.0 * 2 * H),
+                      [&] { return ming::launch_adaln_glue_batch(gl, c->stream); }),
+             "batched adaLN glue launch");
+    // counted as the per-block projections and glue are
+    if (q0->bits == 4) c->eng.gemm_q4 += nb;
+    else if (q0->bits == 8) c->eng.gemm_q8 += nb;
+    else c->eng.gemm_dense += nb;
+    c->eng.gemv += nb;
+    c->eng.gemm_flops += 2ull * (uint64_t)nb * (uint64_t)q0->N * (uint64_t)q0->K;
+    c->eng.elementwise += nb;
+  }
+  *done = true;
+  return ok();
+}
+
 int rt_tanh_gates(ming_ctx* c, const uint16_t* mods, int n, float* t) {
   DeviceGuard g(c->device);
   MING_HIP(profiled(c, kBModulate, 0.0, 2.0 * 2 * n + 4.0 * 2 * n,
