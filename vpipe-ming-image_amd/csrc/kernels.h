@@ -150,6 +150,13 @@ hipError_t launch_rope_table(const int32_t* pt, const int32_t* ph,
                              const int32_t* pw, int n, int a0, int a1, int a2,
                              int head_dim, double theta, float* cos_t,
                              float* sin_t, hipStream_t s);
+// h = bf16(h + (tg *) rmsnorm(sub) * wpost) then y = rmsnorm(h) * wpre and
+// yh = fp16(y): the residual modes followed by mode 1, bit for bit, in one pass.
+hipError_t launch_norm_residual_norm(const uint16_t* sub, long long lds, const uint16_t* wpost,
+                                     uint16_t* h, long long ldh, const float* tg,
+                                     const uint16_t* wpre, uint16_t* y, long long ldy,
+                                     uint16_t* yh, long long ldyh, int rows, int D, float eps,
+                                     hipStream_t s);
 hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
                                int k_col, int rows, int n_heads,
                                const uint16_t* wq, const uint16_t* wk,

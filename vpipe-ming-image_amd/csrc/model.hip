@@ -102,11 +102,15 @@ struct Premod {
 
 // run_block (ming-dit.cc:2065-2263) with fill_mod folded in; pm: the
 // block's modulation already computed (rt_modulation_batch), else it is
-// computed here.
+// computed here. prenormed: the previous block's last pass already wrote
+// this block's attention pre-norm (w.nrm and the context's fp16 copy);
+// next_g1: the next block's attention pre-norm weight over the same rows,
+// applied by this block's last pass (then the next block runs prenormed).
 int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& d,
                   uint16_t* x, int rows, const float* cos_t, const float* sin_t,
                   const uint16_t* temb, const float* scales, const BlockWs& w,
-                  const Premod* pm = nullptr) {
+                  const Premod* pm = nullptr, bool prenormed = false,
+                  const uint16_t* next_g1 = nullptr) {
   const int H = d.hidden, F = d.ffn, NH = d.n_heads;
   const bool modulated = b->ada != nullptr;
   const float eps = d.eps;
@@ -128,7 +132,7 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
   }
   // ---- attention half ----
   // the norm also writes the fp16 copy q, k and v read (one conversion, not three)
-  RC(ming::rt_rmsnorm_f16(c, x, H, g1, w.nrm, H, rows, H, eps));
+  if (!prenormed) RC(ming::rt_rmsnorm_f16(c, x, H, g1, w.nrm, H, rows, H, eps));
   {
     const ming_qweight* qkv[3] = {b->q, b->k, b->v};
     uint16_t* out[3] = {w.qkv, w.qkv + H, w.qkv + 2 * H};
@@ -141,12 +145,16 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
   RC(ming::rt_attention_xh(c, w.qkv, 3 * H, 0, H, 2 * H, w.nrm, H, rows, NH,
                            1.0f / std::sqrt(128.0f)));
   RC(ming::rt_lin_xh(c, b->o, w.nrm, H, w.ob, H, rows, scales));
-  // post-norm and the (gated) residual in one pass
-  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->an2, tg, rows, H, eps));
+  // post-norm and the (gated) residual, then the feed-forward half's pre-norm
+  // (and its fp16 copy) of the new stream rows, in one pass
+  RC(ming::rt_norm_residual_norm(c, x, H, w.ob, H, b->an2, tg, g3, w.nrm, H, rows, H, eps));
   // ---- feed-forward half (gpu_ff, 2151-2162; SwiGLU fused into w3) ----
-  RC(ming::rt_rmsnorm_f16(c, x, H, g3, w.nrm, H, rows, H, eps));
   RC(ming::rt_ffn_xh(c, b->w1, b->w3, b->w2, w.nrm, H, w.ob, H, rows, scales, w.ffg, F));
-  RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->fn2, tg ? tg + H : nullptr, rows, H, eps));
+  if (next_g1)
+    RC(ming::rt_norm_residual_norm(c, x, H, w.ob, H, b->fn2, tg ? tg + H : nullptr, next_g1,
+                                   w.nrm, H, rows, H, eps));
+  else
+    RC(ming::rt_norm_residual(c, x, H, w.ob, H, b->fn2, tg ? tg + H : nullptr, rows, H, eps));
   return MING_OK;
 }
 
@@ -684,13 +692,23 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
                                    m->temb, H, mods.data(), nw1.data(), nw3.data(), tg.data(),
                                    nullptr, &premod));
   }
+  bool prenormed = false;
   for (int L = 0; L < NM; ++L) {
     if (stop_requested(m)) return stopped(s);
     prog.poll(false);
     const int rows = L < d.n_refiner ? IMG : JT;
     const Premod pm = premod_of(m->premod, (size_t)H, L);
+    // the next block's pre-norm rides on this block's last pass when it
+    // covers the same rows and its weight is known already
+    const uint16_t* next_g1 = nullptr;
+    if (L + 1 < NM && (L + 1 < d.n_refiner ? IMG : JT) == rows) {
+      const ming_block_desc& nb = m->blocks[(size_t)L + 1];
+      if (!nb.ada) next_g1 = nb.an1;
+      else if (premod) next_g1 = premod_of(m->premod, (size_t)H, L + 1).nw1;
+    }
     RC(block_forward(c, &m->blocks[(size_t)L], bd, m->joint, rows, m->cos_t, m->sin_t,
-                     m->temb, m->scales, w, premod ? &pm : nullptr));
+                     m->temb, m->scales, w, premod ? &pm : nullptr, prenormed, next_g1));
+    prenormed = next_g1 != nullptr;
     RC(prog.done_block(s));
     // with a stop wired, the host stays within 4 blocks of the GPU so that a
     // stop requested mid-forward is seen (ming-dit.cc:2530-2540)

@@ -130,6 +130,125 @@ __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
   }
 }
 
+// The post-norm + residual of MODE 2 (gated) / 3, then MODE 1 on the new
+// stream row, in one pass: h = bf16(h + (tg *) bf16(rms(sub) * wpost)),
+// y = bf16(rms(h) * wpre), yh = fp16(y). The new row is normalized from
+// registers instead of being read back. Every expression and both
+// reductions are rmsnorm_kernel's at the same LPR / CPL, so the result is
+// bit-identical to the two launches it replaces.
+template <int LPR, int CPL, bool GATED>
+__global__ __launch_bounds__(256, 5) void norm_residual_norm_kernel(
+    const uint16_t* sub, long long lds, const uint16_t* __restrict__ wpost,
+    uint16_t* h, long long ldh, const float* __restrict__ tg,
+    const uint16_t* __restrict__ wpre, uint16_t* y, long long ldy, uint16_t* yh,
+    long long ldyh, int rows, int D, float eps) {
+  constexpr int RPW = 64 / LPR;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // rows wave-uniform at LPR 64
+  const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
+  const int sb = lane % LPR;
+  const int nch = D >> 3;
+  const bool live = row < rows;
+  const long long rr = live ? row : 0;
+  uint4 v[CPL], hv[CPL];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = sb + LPR * i;
+    if (live && c < nch) {
+      v[i] = *reinterpret_cast<const uint4*>(sub + rr * lds + 8 * c);
+      hv[i] = *reinterpret_cast<const uint4*>(h + rr * ldh + 8 * c);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = sb + LPR * i;
+    if (live && c < nch) {
+      const uint32_t* u = &v[i].x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = bf16_lo(u[e]), b = bf16_hi(u[e]);
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  // the residual: h += (tg *) bf16(rms(sub) * wpost), kept in hv
+  float ss2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = sb + LPR * i;
+    if (live && c < nch) {
+      const uint4 wv = *reinterpret_cast<const uint4*>(wpost + 8 * c);
+      const uint32_t* u = &v[i].x;
+      const uint32_t* wu = &wv.x;
+      uint32_t ou[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = __fmul_rn(__fmul_rn(bf16_lo(u[e]), inv), bf16_lo(wu[e]));
+        const float b = __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv), bf16_hi(wu[e]));
+        ou[e] = pack_bf16x2_rne(a, b);
+      }
+      float t[8];
+      if constexpr (GATED) {
+        const float4 t0 = *reinterpret_cast<const float4*>(tg + 8 * c);
+        const float4 t1 = *reinterpret_cast<const float4*>(tg + 8 * c + 4);
+        t[0] = t0.x; t[1] = t0.y; t[2] = t0.z; t[3] = t0.w;
+        t[4] = t1.x; t[5] = t1.y; t[6] = t1.z; t[7] = t1.w;
+      }
+      uint32_t* hp = &hv[i].x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float s0 = bf16_lo(ou[e]), s1 = bf16_hi(ou[e]);
+        if constexpr (GATED) {
+          s0 = __fmul_rn(t[2 * e], s0);
+          s1 = __fmul_rn(t[2 * e + 1], s1);
+        }
+        hp[e] = pack_bf16x2_rne(__fadd_rn(bf16_lo(hp[e]), s0), __fadd_rn(bf16_hi(hp[e]), s1));
+      }
+      *reinterpret_cast<uint4*>(h + rr * ldh + 8 * c) = hv[i];
+      // the next norm's sum of squares, in rmsnorm_kernel's order
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = bf16_lo(hp[e]), b = bf16_hi(hp[e]);
+        ss2 = fmaf(a, a, ss2);
+        ss2 = fmaf(b, b, ss2);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = LPR / 2; o >= 1; o >>= 1) ss2 += __shfl_xor(ss2, o, 64);
+  const float inv2 = 1.0f / sqrtf(ss2 / (float)D + eps);
+  if (!live) return;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = sb + LPR * i;
+    if (c < nch) {
+      const uint4 wv = *reinterpret_cast<const uint4*>(wpre + 8 * c);
+      const uint32_t* u = &hv[i].x;
+      const uint32_t* wu = &wv.x;
+      uint4 o;
+      uint32_t* ou = &o.x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = __fmul_rn(__fmul_rn(bf16_lo(u[e]), inv2), bf16_lo(wu[e]));
+        const float b = __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv2), bf16_hi(wu[e]));
+        ou[e] = pack_bf16x2_rne(a, b);
+      }
+      *reinterpret_cast<uint4*>(y + rr * ldy + 8 * c) = o;
+      uint4 f;
+      f.x = bf16x2_to_f16x2(o.x);
+      f.y = bf16x2_to_f16x2(o.y);
+      f.z = bf16x2_to_f16x2(o.z);
+      f.w = bf16x2_to_f16x2(o.w);
+      *reinterpret_cast<uint4*>(yh + rr * ldyh + 8 * c) = f;
+    }
+  }
+}
+
 // cos/sin [n][head_dim/2] from three integer positions per row: pairs
 // [0, a0/2) on axis 0, then a1/2 on axis 1, then a2/2 on axis 2;
 // freq = 1/theta^(2j/d), angle = pos*freq, both f64, stored f32
@@ -245,6 +364,37 @@ hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const u
   return hipGetLastError();
 }
 
+hipError_t launch_norm_residual_norm(const uint16_t* sub, long long lds, const uint16_t* wpost,
+                                     uint16_t* h, long long ldh, const float* tg,
+                                     const uint16_t* wpre, uint16_t* y, long long ldy,
+                                     uint16_t* yh, long long ldyh, int rows, int D, float eps,
+                                     hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  const int nch = D / 8;
+  if (D % 8 != 0 || nch > 64 * 16) return hipErrorInvalidValue;
+#define MING_NRN_G(LPR, CPL, G)                                                          \
+  hipLaunchKernelGGL((norm_residual_norm_kernel<LPR, CPL, G>), dim3((rows + rpb - 1) / rpb), \
+                     dim3(256), 0, s, sub, lds, wpost, h, ldh, tg, wpre, y, ldy, yh, ldyh,   \
+                     rows, D, eps)
+#define MING_NRN(LPR, CPL)                                                     \
+  do {                                                                         \
+    const int rpb = 4 * (64 / (LPR));                                          \
+    if (tg) MING_NRN_G(LPR, CPL, true);                                        \
+    else MING_NRN_G(LPR, CPL, false);                                          \
+  } while (0)
+  // the (LPR, CPL) choice of launch_rmsnorm_ex: the same reductions
+  if (nch <= 8) MING_NRN(8, 1);
+  else if (nch <= 16) MING_NRN(16, 1);
+  else if (nch <= 32) MING_NRN(32, 1);
+  else if (nch <= 64) MING_NRN(64, 1);
+  else if (nch <= 256) MING_NRN(64, 4);
+  else if (nch <= 512) MING_NRN(64, 8);
+  else MING_NRN(64, 16);
+#undef MING_NRN
+#undef MING_NRN_G
+  return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
                           uint16_t* y, long long ldy, int rows, int D,
                           float eps, hipStream_t s) {
@@ -291,6 +441,12 @@ hipError_t validate_norm_kernels() {
       MING_RMS_ALL(8, 1),  MING_RMS_ALL(16, 1), MING_RMS_ALL(32, 1), MING_RMS_ALL(64, 1),
       MING_RMS_ALL(64, 4), MING_RMS_ALL(64, 8), MING_RMS_ALL(64, 16),
 #undef MING_RMS_ALL
+#define MING_NRN_ALL(LPR, CPL)                                                  \
+  reinterpret_cast<const void*>(&norm_residual_norm_kernel<LPR, CPL, true>),    \
+      reinterpret_cast<const void*>(&norm_residual_norm_kernel<LPR, CPL, false>)
+      MING_NRN_ALL(8, 1),  MING_NRN_ALL(16, 1), MING_NRN_ALL(32, 1), MING_NRN_ALL(64, 1),
+      MING_NRN_ALL(64, 4), MING_NRN_ALL(64, 8), MING_NRN_ALL(64, 16),
+#undef MING_NRN_ALL
       reinterpret_cast<const void*>(&rope_table_kernel),
       reinterpret_cast<const void*>(&qk_norm_rope_kernel)};
   for (const void* f : fns) {

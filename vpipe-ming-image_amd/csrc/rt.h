@@ -55,6 +55,12 @@ int rt_ffn_xh(ming_ctx* c, const ming_qweight* w1, const ming_qweight* w3,
 int rt_norm_residual(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
                      int64_t lds, const uint16_t* w, const float* tgate, int rows, int D,
                      float eps);
+// rt_norm_residual followed by rt_rmsnorm_f16 on the new h (weight wpre, into
+// y and the context's fp16 copy), bit for bit, in one pass over the rows.
+int rt_norm_residual_norm(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
+                          int64_t lds, const uint16_t* wpost, const float* tgate,
+                          const uint16_t* wpre, uint16_t* y, int64_t ldy, int rows, int D,
+                          float eps);
 // t[0, n) = tanh(mods[n, 2n)), t[n, 2n) = tanh(mods[3n, 4n)) in f32: a block's
 // two residual gates, once per block instead of once per element.
 int rt_tanh_gates(ming_ctx* c, const uint16_t* mods, int n, float* t);

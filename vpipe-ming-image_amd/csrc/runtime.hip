@@ -1499,6 +1499,34 @@ int rt_norm_residual(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
                   "post-norm residual");
 }
 
+int rt_norm_residual_norm(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t* sub,
+                          int64_t lds, const uint16_t* wpost, const float* tgate,
+                          const uint16_t* wpre, uint16_t* y, int64_t ldy, int rows, int D,
+                          float eps) {
+  if (!c || !h || !sub || !wpost || !wpre || !y)
+    return fail(MING_ERR_ARG, "norm-residual-norm: null argument");
+  if (rows < 0 || D <= 0 || D % 8 != 0 || D > 8192 || ldh < D || ldh % 8 != 0 || lds < D ||
+      lds % 8 != 0 || ldy < D || ldy % 8 != 0)
+    return fail(MING_ERR_SHAPE, "norm-residual-norm: bad shape or row strides");
+  if (!aligned(h, 16) || !aligned(sub, 16) || !aligned(wpost, 16) || !aligned(wpre, 16) ||
+      !aligned(y, 16) || (tgate && !aligned(tgate, 16)))
+    return fail(MING_ERR_ARG, "norm-residual-norm: pointers must be 16-byte aligned");
+  if (rows == 0) return ok();
+  DeviceGuard g(c->device);
+  int rc = ensure_xh(c, (size_t)rows * D * 2);
+  if (rc != MING_OK) return rc;
+  uint16_t* yh = (uint16_t*)c->xh;
+  MING_HIP(profiled(c, kBNormRes, 0.0, 10.0 * rows * D + (tgate ? 8.0 : 4.0) * D,
+                    [&] { return ming::launch_norm_residual_norm(sub, lds, wpost, h, ldh, tgate,
+                                                                 wpre, y, ldy, yh, D, rows, D,
+                                                                 eps, c->stream); }),
+           "norm-residual-norm launch");
+  // counted as the two launches it replaces
+  c->eng.rmsnorm += 2;
+  c->eng.elementwise += 1;
+  return ok();
+}
+
 int rt_adaln_glue(ming_ctx* c, uint16_t* mods, int n, const uint16_t* b, const uint16_t* an1,
                   const uint16_t* fn1, uint16_t* nw1, uint16_t* nw3, float* t) {
   DeviceGuard g(c->device);
