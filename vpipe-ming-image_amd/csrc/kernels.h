@@ -29,7 +29,7 @@ struct QprojSeg {
   int n_begin;          // first output column of this segment
   int n_end;
   int t_col0;           // first T column of this segment's live ranks
-  int chunks;           // live rank chunks of 64 (0: no adapter)
+  int chunks;           // live rank chunks of 32 (0: no adapter)
   int ldb;
   int grp0;             // first entry of this segment in grp[]
   const uint16_t* B;    // row (n - n_begin)

@@ -115,7 +115,10 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
   for (int i = 1; i < a.nseg; ++i)
     if (n0 >= a.seg[i].n_begin) sg = i;
   const int t_col0 = a.seg[sg].t_col0;
-  const int chunks = a.seg[sg].chunks;
+  // the tail runs in 64-rank steps; an odd count of 32-rank chunks leaves
+  // the upper half of the last step as zeros (T and B both)
+  const int chunks32 = a.seg[sg].chunks;
+  const int chunks = (chunks32 + 1) / 2;
   const int ldb = a.seg[sg].ldb;
   const int grp0 = a.seg[sg].grp0;
   const int seg_nb = a.seg[sg].n_begin, seg_ne = a.seg[sg].n_end;
@@ -200,13 +203,15 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
   // ---- tail stage: T chunk + gathered B chunk ----
   auto load_tail = [&](int ch) {
     const int tc = t_col0 + ch * 64 + pc * 8;
+    const bool in = ch * 64 + pc * 8 < 32 * chunks32;   // inside the segment's ranks
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       int m = m0 + pr + 32 * i;
       m = m < mlast ? m : mlast;
-      xr[i] = *reinterpret_cast<const uint4*>(a.t + (long long)m * a.ldt + tc);
+      xr[i] = in ? *reinterpret_cast<const uint4*>(a.t + (long long)m * a.ldt + tc)
+                 : make_uint4(0, 0, 0, 0);
     }
-    const int g = a.grp[grp0 + ch * 4 + (pc >> 1)];
+    const int g = in ? a.grp[grp0 + ch * 4 + (pc >> 1)] : -1;
     const int bc = (g < 0 ? 0 : g * 16) + (pc & 1) * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {

@@ -383,7 +383,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
   int sg = 0;
   for (int i = 1; i < a.nseg; ++i)
     if (n0 >= a.seg[i].n_begin) sg = i;
-  const int chunks32 = 2 * a.seg[sg].chunks;
+  const int chunks32 = a.seg[sg].chunks;
   if (chunks32 > 0) {
     const int t_col0 = a.seg[sg].t_col0;
     const int ldb = a.seg[sg].ldb;
@@ -417,7 +417,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
       for (int i = 0; i < 4; ++i)
         dma16_sb(a.t + 32 * ch, toff[i], lds_addr(X + 64 * (4 * wave + i)));
       // The chunk's two groups are one aligned dword of the table (a
-      // segment's groups start at a multiple of 4): a wave-uniform scalar
+      // segment's groups start at a multiple of 2): a wave-uniform scalar
       // load (lgkmcnt), never a VMEM load the compiler would wait for with
       // vmcnt(0) behind the ring's DMAs.
       const int gi = __builtin_amdgcn_readfirstlane(grp0 + 2 * ch);

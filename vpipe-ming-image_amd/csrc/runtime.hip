@@ -862,8 +862,8 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       }
       if (seg_groups == 0) continue;
       ++live_segs[i];
-      // pad the segment's T columns to whole 64-wide chunks with zero groups
-      const int padded = round_up(seg_groups, 4);
+      // pad the segment's T columns to whole 32-rank chunks with zero groups
+      const int padded = round_up(seg_groups, 2);
       for (int gi = seg_groups; gi < padded; ++gi) {
         if (xa_groups + gi >= ming::kMaxGroups || qp_groups + gi >= ming::kMaxGroups)
           return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
@@ -871,10 +871,19 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
         xa.coef[xa_groups + gi] = 0.0f;
         qa[i].grp[qp_groups + gi] = -1;
       }
-      d.chunks = padded / 4;
+      d.chunks = padded / 2;
       xa_groups += padded;
       qp_groups += padded;
     }
+  }
+  // the x.A kernels write T in 64-column blocks: zero groups after the last
+  // segment make the stack a whole number of them
+  while (xa_groups % 4 != 0) {
+    if (xa_groups >= ming::kMaxGroups)
+      return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
+    xa.grp[xa_groups] = -1;
+    xa.coef[xa_groups] = 0.0f;
+    ++xa_groups;
   }
   const int t_cols = xa_groups * 16;
   uint16_t* T = nullptr;
