@@ -252,17 +252,28 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
   const std::integral_constant<bool, false> whole{};
   const std::integral_constant<bool, true> last{};
 
+  // Steady state: pairs of unmasked steps with no branch between them (a
+  // step that may be the last one inside the loop made the compiler copy the
+  // loop-carried accumulators at every step); then the one or two steps left,
+  // the last one masked.
   issue(0, sk0, sv0);
-  for (int kb = 0; kb < NKB; kb += 2) {
+  int kb = 0;
+  for (; kb + 2 < NKB; kb += 2) {
     attn_sync();                                   // stage kb landed; sk1/sv1 free
-    issue(kb + 1 < NKB ? kb + 1 : NKB - 1, sk1, sv1);
-    if (kb + 1 < NKB) step(whole, kb, sk0, sv0);
-    else step(last, kb, sk0, sv0);
-    if (kb + 1 >= NKB) break;
+    issue(kb + 1, sk1, sv1);
+    step(whole, kb, sk0, sv0);
     attn_sync();
-    issue(kb + 2 < NKB ? kb + 2 : NKB - 1, sk0, sv0);
-    if (kb + 2 < NKB) step(whole, kb + 1, sk1, sv1);
-    else step(last, kb + 1, sk1, sv1);
+    issue(kb + 2, sk0, sv0);
+    step(whole, kb + 1, sk1, sv1);
+  }
+  attn_sync();                                     // stage kb landed
+  if (kb + 1 < NKB) {
+    issue(kb + 1, sk1, sv1);
+    step(whole, kb, sk0, sv0);
+    attn_sync();
+    step(last, kb + 1, sk1, sv1);
+  } else {
+    step(last, kb, sk0, sv0);
   }
   attn_sync();                                     // no DMA outlives the block
 
