@@ -88,10 +88,43 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const uint4*>(qp + 16 * s);
   }
+  // With a.qw, q is the raw projection output: its per-head RMSNorm + RoPE
+  // (launch_qk_norm_rope's arithmetic) is applied here. The lane holds the
+  // 8-column groups 2s + fh of its query; the head's reduction tree (groups
+  // at distance 8, 4, 2, 1) is s ^ 4, s ^ 2, s ^ 1 in registers, then the
+  // other lane half. Weights and table rows load beside q.
+  uint4 qwv[8];
+  float4 qcs[8], qsn[8];
+  if (a.qw) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      qwv[s] = *reinterpret_cast<const uint4*>(a.qw + 16 * s + 8 * fh);
+      qcs[s] = *reinterpret_cast<const float4*>(a.cos_t + (long long)qr * 64 + 8 * s + 4 * fh);
+      qsn[s] = *reinterpret_cast<const float4*>(a.sin_t + (long long)qr * 64 + 8 * s + 4 * fh);
+    }
+  }
   // Wait for them here (vmcnt(0); expcnt, lgkmcnt open): the compiler then
   // puts no wait for them into the key loop, where a vmcnt wait would also
   // wait for the ring's DMA of the next tile, every step.
   __builtin_amdgcn_s_waitcnt(0x0F70);
+  if (a.qw) {
+    float t8[8], t4[8], t2[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) t8[s] = head_ss8(qf[s]);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) t4[s] = t8[s] + t8[s ^ 4];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) t2[s] = t4[s] + t4[s ^ 2];
+    const float t1 = t2[0] + t2[1];
+    const float inv = head_rms_inv(t1 + xor32(t1), a.eps);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      qf[s].x = norm_rope_pair(qf[s].x, qwv[s].x, inv, qcs[s].x, qsn[s].x);
+      qf[s].y = norm_rope_pair(qf[s].y, qwv[s].y, inv, qcs[s].y, qsn[s].y);
+      qf[s].z = norm_rope_pair(qf[s].z, qwv[s].z, inv, qcs[s].z, qsn[s].z);
+      qf[s].w = norm_rope_pair(qf[s].w, qwv[s].w, inv, qcs[s].w, qsn[s].w);
+    }
+  }
 
   // DMA offsets (bytes from the step's base). K: chunk p -> row p >> 4,
   // logical chunk (p & 15) ^ (row & 15). V^T: chunk p -> row p >> 3,

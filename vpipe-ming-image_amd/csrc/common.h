@@ -71,6 +71,38 @@ __device__ __forceinline__ uint32_t f32x2_to_f16x2_rne(float a, float b) {
          ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
 }
 
+// Per-head RMSNorm + RoPE of q and k (the qk-norm then the interleaved-pair
+// rotation), shared by qk_norm_rope_kernel and the attention kernel's Q
+// prologue so both give the same bits. A head's sum of squares is the
+// sixteen 8-element chains (eight consecutive elements, fmaf in order)
+// added pairwise at group distance 8, 4, 2, 1.
+__device__ __forceinline__ float head_ss8(const uint4& v) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = bf16_lo(u[e]), b = bf16_hi(u[e]);
+    ss = fmaf(a, a, ss);
+    ss = fmaf(b, b, ss);
+  }
+  return ss;
+}
+__device__ __forceinline__ float head_rms_inv(float ss, float eps) {
+  return 1.0f / sqrtf(ss * (1.0f / 128.0f) + eps);
+}
+// One interleaved pair (x0, x1): normalized with weight pair w, rounded to
+// bf16 (the reference stores the norm), rotated by (c, s) as
+// (x0 + i x1)(c + i s), packed to bf16.
+__device__ __forceinline__ uint32_t norm_rope_pair(uint32_t u, uint32_t w, float inv, float c,
+                                                   float s) {
+  const uint32_t nb = pack_bf16x2_rne(__fmul_rn(__fmul_rn(bf16_lo(u), inv), bf16_lo(w)),
+                                      __fmul_rn(__fmul_rn(bf16_hi(u), inv), bf16_hi(w)));
+  const float a = bf16_lo(nb), b = bf16_hi(nb);
+  const float re = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+  const float im = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+  return pack_bf16x2_rne(re, im);
+}
+
 __device__ __forceinline__ float warp_sum(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -74,6 +74,13 @@ struct AttnArgs {
   int ldv;
   uint16_t* o;
   long long ldo;
+  // optional per-head RMSNorm + RoPE of q, applied to the Q fragments as
+  // they are loaded (launch_qk_norm_rope's arithmetic and bits): weight
+  // qw[128], tables [R][64]; q is then the raw projection output
+  const uint16_t* qw;
+  const float* cos_t;
+  const float* sin_t;
+  float eps;
   // optional fp16 copy of O (the same bf16 values), [R][NH*128] at ldoh: the
   // fast projection route's input for the o-projection
   uint16_t* oh;
@@ -157,6 +164,10 @@ hipError_t launch_norm_residual_norm(const uint16_t* sub, long long lds, const u
                                      const uint16_t* wpre, uint16_t* y, long long ldy,
                                      uint16_t* yh, long long ldyh, int rows, int D, float eps,
                                      hipStream_t s);
+// The same on k alone (the attention kernel norms q itself).
+hipError_t launch_k_norm_rope(uint16_t* x, long long ld, int k_col, int rows, int n_heads,
+                              const uint16_t* wk, const float* cos_t, const float* sin_t,
+                              float eps, hipStream_t s);
 hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
                                int k_col, int rows, int n_heads,
                                const uint16_t* wq, const uint16_t* wk,

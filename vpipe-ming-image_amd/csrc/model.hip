@@ -138,12 +138,11 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
     uint16_t* out[3] = {w.qkv, w.qkv + H, w.qkv + 2 * H};
     RC(ming::rt_lin3_xh(c, qkv, w.nrm, H, out, 3 * H, rows, scales));
   }
-  RC(ming_qk_norm_rope(c, w.qkv, 3 * H, 0, H, rows, NH, 128, b->nq, b->nk, cos_t, sin_t,
-                       eps));
-  // the attention output reuses the normed-input plane (its q/k/v are done);
+  // qk-norm + RoPE: k in one pass, q inside the attention kernel. The
+  // attention output reuses the normed-input plane (its q/k/v are done);
   // its fp16 copy is the o-projection's input
-  RC(ming::rt_attention_xh(c, w.qkv, 3 * H, 0, H, 2 * H, w.nrm, H, rows, NH,
-                           1.0f / std::sqrt(128.0f)));
+  RC(ming::rt_attention_qknorm_xh(c, w.qkv, 3 * H, 0, H, 2 * H, w.nrm, H, rows, NH,
+                                  1.0f / std::sqrt(128.0f), b->nq, b->nk, cos_t, sin_t, eps));
   RC(ming::rt_lin_xh(c, b->o, w.nrm, H, w.ob, H, rows, scales));
   // post-norm and the (gated) residual, then the feed-forward half's pre-norm
   // (and its fp16 copy) of the new stream rows, in one pass

@@ -285,49 +285,31 @@ __global__ void rope_table_kernel(const int32_t* pt, const int32_t* ph,
 // every load is issued before the reduction.
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     uint16_t* __restrict__ x, long long ld, int q_col, int k_col, int rows,
-    int n_heads, const uint16_t* __restrict__ wq,
+    int nq, int nk, const uint16_t* __restrict__ wq,
     const uint16_t* __restrict__ wk, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, float eps) {
   const int tid = threadIdx.x, lane = tid & 63;
   for (int row = (int)blockIdx.y; row < rows; row += (int)gridDim.y) {
   const int hh0 = (int)blockIdx.x * 16 + (tid >> 4);
   const int sub = lane & 15;
-  const bool live = hh0 < 2 * n_heads;
+  const bool live = hh0 < nq + nk;
   const int hh = live ? hh0 : 0;
-  const bool isk = hh >= n_heads;
-  const int head = isk ? hh - n_heads : hh;
+  const bool isk = hh >= nq;
+  const int head = isk ? hh - nq : hh;
   uint16_t* p = x + (long long)row * ld + (isk ? k_col : q_col) + head * 128 + 8 * sub;
   const uint4 v = *reinterpret_cast<const uint4*>(p);
   const uint4 wv = *reinterpret_cast<const uint4*>((isk ? wk : wq) + 8 * sub);
   const float4 cv = *reinterpret_cast<const float4*>(cos_t + (long long)row * 64 + 4 * sub);
   const float4 sv = *reinterpret_cast<const float4*>(sin_t + (long long)row * 64 + 4 * sub);
-  const uint32_t* u = &v.x;
-  float ss = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float a = bf16_lo(u[e]), b = bf16_hi(u[e]);
-    ss = fmaf(a, a, ss);
-    ss = fmaf(b, b, ss);
-  }
+  float ss = head_ss8(v);
 #pragma unroll
   for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  const float inv = 1.0f / sqrtf(ss * (1.0f / 128.0f) + eps);
-  const uint32_t* wu = &wv.x;
-  const float cs[4] = {cv.x, cv.y, cv.z, cv.w};
-  const float sn[4] = {sv.x, sv.y, sv.z, sv.w};
+  const float inv = head_rms_inv(ss, eps);
   uint4 o;
-  uint32_t* ou = &o.x;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    // the norm, rounded to bf16 as the reference stores it
-    const uint32_t nb = pack_bf16x2_rne(__fmul_rn(__fmul_rn(bf16_lo(u[e]), inv), bf16_lo(wu[e])),
-                                        __fmul_rn(__fmul_rn(bf16_hi(u[e]), inv), bf16_hi(wu[e])));
-    const float a = bf16_lo(nb), b = bf16_hi(nb);
-    // (a + i b)(c + i s)
-    const float re = __fsub_rn(__fmul_rn(a, cs[e]), __fmul_rn(b, sn[e]));
-    const float im = __fadd_rn(__fmul_rn(a, sn[e]), __fmul_rn(b, cs[e]));
-    ou[e] = pack_bf16x2_rne(re, im);
-  }
+  o.x = norm_rope_pair(v.x, wv.x, inv, cv.x, sv.x);
+  o.y = norm_rope_pair(v.y, wv.y, inv, cv.y, sv.y);
+  o.z = norm_rope_pair(v.z, wv.z, inv, cv.z, sv.z);
+  o.w = norm_rope_pair(v.w, wv.w, inv, cv.w, sv.w);
   if (live) *reinterpret_cast<uint4*>(p) = o;
   }
 }
@@ -422,8 +404,19 @@ hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
   if (rows <= 0 || n_heads <= 0) return hipSuccess;
   const unsigned gy = (unsigned)(rows < 65535 ? rows : 65535);   // grid y limit; rows stride
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((2 * n_heads + 15) / 16), gy),
-                     dim3(256), 0, s, x, ld, q_col, k_col, rows, n_heads, wq,
+                     dim3(256), 0, s, x, ld, q_col, k_col, rows, n_heads, n_heads, wq,
                      wk, cos_t, sin_t, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_k_norm_rope(uint16_t* x, long long ld, int k_col, int rows, int n_heads,
+                              const uint16_t* wk, const float* cos_t, const float* sin_t,
+                              float eps, hipStream_t s) {
+  if (rows <= 0 || n_heads <= 0) return hipSuccess;
+  const unsigned gy = (unsigned)(rows < 65535 ? rows : 65535);
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((n_heads + 15) / 16), gy),
+                     dim3(256), 0, s, x, ld, k_col, k_col, rows, 0, n_heads, wk, wk,
+                     cos_t, sin_t, eps);
   return hipGetLastError();
 }
 

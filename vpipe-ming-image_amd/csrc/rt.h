@@ -42,6 +42,13 @@ int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ld
 int rt_attention_xh(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int k_col,
                     int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
                     float scale);
+// rt_attention_xh on raw q and k projection outputs: ming_qk_norm_rope's per-
+// head RMSNorm + RoPE is applied to k by one pass (in place) and to q inside
+// the attention kernel as it loads it, with the same bits.
+int rt_attention_qknorm_xh(ming_ctx* c, uint16_t* qkv, int64_t ld, int q_col, int k_col,
+                           int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
+                           float scale, const uint16_t* wq, const uint16_t* wk,
+                           const float* cos_t, const float* sin_t, float eps);
 // the three projections q, k, v over the same normed x, one x.A launch for
 // their adapters, outputs y[i] with one row stride
 int rt_lin3_xh(ming_ctx* c, const ming_qweight* const* qw, const uint16_t* x, int64_t ldx,

@@ -1185,9 +1185,18 @@ int ming_qk_norm_rope(ming_ctx* c, uint16_t* x, int64_t ld, int q_col, int k_col
 
 // oh: optional fp16 copy of the output (the context's xh plane, row stride
 // n_heads * 128) for the o-projection's fast route.
+// qn: q and k arrive as raw projection outputs; k is normed + rotated in
+// place by one pass, q by the attention kernel as it loads it (the bits of
+// ming_qk_norm_rope followed by ming_attention).
+struct QkNorm {
+  const uint16_t *wq, *wk;
+  const float *cos_t, *sin_t;
+  float eps;
+};
 static int attention_impl(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int k_col,
                           int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
-                          int head_dim, float scale, bool fp16_copy) {
+                          int head_dim, float scale, bool fp16_copy,
+                          const QkNorm* qn = nullptr) {
   if (!c || !qkv || !out) return fail(MING_ERR_ARG, "ming_attention: null argument");
   if (head_dim != 128)
     return fail(MING_ERR_SHAPE, "ming_attention: head_dim must be 128");
@@ -1221,6 +1230,19 @@ static int attention_impl(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_co
   }
   a.R = rows; a.NH = n_heads;
   a.sl2 = scale * 1.4426950408889634f;
+  if (qn) {
+    if (!qn->wq || !qn->wk || !qn->cos_t || !qn->sin_t || !aligned(qn->wq, 16) ||
+        !aligned(qn->wk, 16) || !aligned(qn->cos_t, 16) || !aligned(qn->sin_t, 16))
+      return fail(MING_ERR_ARG, "attention: bad qk-norm weights or tables");
+    uint16_t* kx = const_cast<uint16_t*>(qkv);
+    MING_HIP(profiled(c, kBQkRope, 0.0, 4.0 * rows * w + 256.0,
+                      [&] { return ming::launch_k_norm_rope(kx, ld, k_col, rows, n_heads,
+                                                            qn->wk, qn->cos_t, qn->sin_t,
+                                                            qn->eps, c->stream); }),
+             "k-norm launch");
+    c->eng.qk_norm_rope += 1;
+    a.qw = qn->wq; a.cos_t = qn->cos_t; a.sin_t = qn->sin_t; a.eps = qn->eps;
+  }
   const double flops = 4.0 * (double)rows * rows * 128.0 * n_heads;
   MING_HIP(profiled(c, kBAttn, flops, 8.0 * rows * w,
                     [&] { return ming::launch_attention(a, qkv + v_col, ld, c->stream); }),
@@ -1619,6 +1641,15 @@ int rt_attention_xh(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int
                     float scale) {
   return attention_impl(c, qkv, ld, q_col, k_col, v_col, out, ldo, rows, n_heads, 128, scale,
                         true);
+}
+
+int rt_attention_qknorm_xh(ming_ctx* c, uint16_t* qkv, int64_t ld, int q_col, int k_col,
+                           int v_col, uint16_t* out, int64_t ldo, int rows, int n_heads,
+                           float scale, const uint16_t* wq, const uint16_t* wk,
+                           const float* cos_t, const float* sin_t, float eps) {
+  const QkNorm qn{wq, wk, cos_t, sin_t, eps};
+  return attention_impl(c, qkv, ld, q_col, k_col, v_col, out, ldo, rows, n_heads, 128, scale,
+                        true, &qn);
 }
 
 int rt_lin_xh(ming_ctx* c, const ming_qweight* qw, const uint16_t* x, int64_t ldx,
