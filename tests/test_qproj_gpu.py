@@ -365,3 +365,57 @@ def test_dense_few_tiles_parity(ctx, orc, M, N, K):
     ref = orc.proj(np.ascontiguousarray(x[:, :K]), w)
     assert _rel(orc, np.ascontiguousarray(out[:, :N]), ref) <= TOL
     qw.close()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_few_tiles_split_k_parity(ctx, orc, bits):
+    """A fast-route projection over 256 rows (the context refiner's caption
+    rows: 15 tiles of 256 x 256) splits K across the chip, the last slice
+    carrying the LoRA tail: to the bar against the fp32 reference with the
+    config-2 adapter set (the route fixture runs the unsplit general kernel
+    on it as well)."""
+    M, N, K = 256, 3840, 3840
+    print(f"case split bits={bits} M={M} N={N} K={K}", flush=True)
+    x = bf16(randn(41, (M, K)))
+    pack, w = make_weight(42, N, K, bits)
+    qw = _qw(ctx, pack, bits)
+    loras = []
+    for s, r in enumerate(CFG2_RANKS):
+        A, B = make_lora(300 + 2 * s, N, K, r)
+        qw.bind_lora(s, A, B)
+        loras.append((A, B, CFG2_SCALES[s]))
+    ctx.reset_engagement()
+    y = _run(ctx, qw, to_dev(x), M, CFG2_SCALES)
+    eng = ctx.engagement()
+    assert eng["lora_proj"] == 1 and eng["gemm_fast"] == (1 if route_is_auto(ctx) else 0)
+    ref = orc.proj(x, w, loras)
+    assert _rel(orc, y, ref) <= TOL
+    assert orc.rel_l2(ref, orc.proj(x, w)) > 10 * TOL
+    qw.close()
+
+
+def test_few_tiles_ffn_equals_the_four_calls(ctx):
+    """ming_ffn over 256 rows at full width (w1, w3: 40 tiles, w2: 15, all
+    split on the fast route; the split reduce applies w3's SwiGLU and writes
+    the fp16 copy of h) == lin(w1), lin(w3), swiglu, lin(w2) bit for bit."""
+    M, H, F = 256, 3840, 10240
+    w1, w3, w2 = _ffn_weights(ctx, 640, H, F)
+    x = to_dev(bf16(randn(641, (M, H))))
+    g = to_dev(_run(ctx, w1, x, M, CFG2_SCALES))
+    u = to_dev(_run(ctx, w3, x, M, CFG2_SCALES))
+    a = empty_bf16(M, F)
+    sync()
+    ctx.swiglu(g, u, a, M, F)
+    sync()
+    ref = _run(ctx, w2, a, M, CFG2_SCALES)
+    y = empty_bf16(M, H)
+    ctx.ffn(w1, w3, w2, x, y, M, CFG2_SCALES)
+    sync()
+    assert np.array_equal(from_dev(y), ref)
+    assert np.all(np.isfinite(orc_f32(from_dev(y))))
+    for wt in (w1, w3, w2):
+        wt.close()
+
+
+def orc_f32(v):
+    return (v.astype(np.uint32) << 16).view(np.float32)

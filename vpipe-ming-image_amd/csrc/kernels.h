@@ -57,6 +57,10 @@ struct QprojArgs {
   long long ldyh;
   QprojSeg seg[kMaxSeg];
   int16_t grp[kMaxGroups];
+  // fast route, split K (kslices > 1): f32 partials [kslices][M][N] in part,
+  // summed in slice order by a second launch (N % 4 == 0)
+  float* part;
+  int kslices;
 };
 
 hipError_t launch_qproj(int bits, const QprojArgs& a, hipStream_t s);

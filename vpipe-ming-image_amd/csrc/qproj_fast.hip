@@ -151,7 +151,11 @@ __device__ __forceinline__ int wchunk(int n, int h) {
   return n * CPR + (h ^ wswz<CPR>(n));
 }
 
-template <int BITS>
+// SPLIT (a.kslices > 1, a projection of few tiles): block b is slice
+// b / tiles of tile b % tiles. The slice runs its share of K (the last one
+// also the LoRA tail) and writes f32 partials to a.part; the split reduce
+// then sums the slices in order and finishes as the epilogue does.
+template <int BITS, bool SPLIT>
 __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
   constexpr int WCH = BITS == 4 ? 512 : 1024;    // 16-B code chunks per stage
   constexpr int CPR = BITS == 4 ? 2 : 4;         // code chunks per row
@@ -171,14 +175,23 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 
   const int tiles_m = (a.M + BM - 1) / BM;
   const int tiles_n = (a.N + BN - 1) / BN;
-  int tm, tn;
-  tile_of_block(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  int tm, tn, blk = (int)blockIdx.x, ks = 0, kt0 = 0;
+  int KT = a.K / BK;
+  if constexpr (SPLIT) {
+    ks = blk / (tiles_m * tiles_n);
+    blk -= ks * (tiles_m * tiles_n);
+    kt0 = KT * ks / a.kslices;
+    KT = KT * (ks + 1) / a.kslices - kt0;
+  }
+  tile_of_block(blk, tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = a.K / BK;
   const int mlast = a.M - 1, nlast = a.N - 1;
 
-  const _Float16* __restrict__ x16 = reinterpret_cast<const _Float16*>(a.x);
-  const uint4* __restrict__ codes = reinterpret_cast<const uint4*>(a.codes);
+  // stage 0 of this block's K range
+  const _Float16* __restrict__ x16 = reinterpret_cast<const _Float16*>(a.x) + (long long)kt0 * BK;
+  const uint4* __restrict__ codes =
+      reinterpret_cast<const uint4*>(a.codes) + (long long)kt0 * a.N * CPR;
+  const uint32_t* __restrict__ sbp = a.sb + (long long)kt0 * a.N;
 
   // DMA sources for this lane, per stage (advance by k).
   // x tile: wave issues chunks q = 8*wave + i; lane p = 64q + lane.
@@ -222,7 +235,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 #pragma unroll
       for (int i = 0; i < WDMA; ++i)
         dma16_sb(wbase, woff[i], lds_addr(B + BM * 8 + 64 * (WDMA * wave + i)));
-      dma4_sb(a.sb + (long long)kt * a.N, soff,
+      dma4_sb(sbp + (long long)kt * a.N, soff,
               lds_addr(reinterpret_cast<const uint32_t*>(B + BM * 8 + WCH) + 64 * wave));
     }
   };
@@ -383,7 +396,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
   int sg = 0;
   for (int i = 1; i < a.nseg; ++i)
     if (n0 >= a.seg[i].n_begin) sg = i;
-  const int chunks32 = a.seg[sg].chunks;
+  const int chunks32 = (!SPLIT || ks == a.kslices - 1) ? a.seg[sg].chunks : 0;
   if (chunks32 > 0) {
     const int t_col0 = a.seg[sg].t_col0;
     const int ldb = a.seg[sg].ldb;
@@ -491,6 +504,26 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     ring_wait<0>();
   }
 
+  if constexpr (SPLIT) {
+    // f32 partials P[ks][m][n]: lane row 32i + fr, four columns per quad
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int m = m0 + 32 * i + fr;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + 64 * wave + 32 * j + 8 * q + 4 * fk;
+          if (n < a.N)
+            *reinterpret_cast<float4*>(a.part + ((long long)ks * a.M + m) * a.N + n) =
+                make_float4(acc[j][i][4 * q + 0], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
+                            acc[j][i][4 * q + 3]);
+        }
+    }
+    return;
+  }
+
   // Epilogue through LDS: each wave converts its 64 columns x 128 rows at a
   // time to bf16 in its own 16 KB region (rows of 128 B, chunks swizzled by
   // (row >> 1) & 7 so both the 8-B writes and the 16-B reads are
@@ -563,6 +596,36 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
         }
       }
     }
+  }
+}
+
+// The split projection's end: y = bf16(sum of the slices in order), then as
+// the epilogue: the fused SwiGLU bf16(silu(g) * y) and the fp16 copy.
+__global__ void qproj_split_reduce_kernel(const QprojArgs a) {
+  const int n4 = a.N >> 2;
+  const long long total = (long long)a.M * n4;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long m = i / n4;
+    const int n = (int)(i % n4) * 4;
+    float4 sum = *reinterpret_cast<const float4*>(a.part + m * a.N + n);
+    for (int k = 1; k < a.kslices; ++k) {
+      const float4 v = *reinterpret_cast<const float4*>(a.part + ((long long)k * a.M + m) * a.N + n);
+      sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+    }
+    uint32_t vp[2] = {pack_bf16x2_rne(sum.x, sum.y), pack_bf16x2_rne(sum.z, sum.w)};
+    if (a.g) {
+      const uint2 gv = *reinterpret_cast<const uint2*>(a.g + m * a.ldg + n);
+      const uint32_t gp[2] = {gv.x, gv.y};
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        vp[e] = pack_bf16x2_rne(silu_f(bf16_lo(gp[e])) * bf16_lo(vp[e]),
+                                silu_f(bf16_hi(gp[e])) * bf16_hi(vp[e]));
+    }
+    *reinterpret_cast<uint2*>(a.y + m * a.ldy + n) = make_uint2(vp[0], vp[1]);
+    if (a.yh)
+      *reinterpret_cast<uint2*>(a.yh + m * a.ldyh + n) =
+          make_uint2(bf16x2_to_f16x2(vp[0]), bf16x2_to_f16x2(vp[1]));
   }
 }
 
@@ -865,10 +928,26 @@ __global__ void bf16_to_f16_kernel(const uint16_t* x, long long ldx, uint16_t* y
 hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return hipSuccess;
+  if (a.kslices > 1) {
+    if (!a.part || a.N % 4 != 0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(tiles * a.kslices));
+    if (bits == 4)
+      hipLaunchKernelGGL((qproj_fast_kernel<4, true>), grid, dim3(256), 0, s, a);
+    else if (bits == 8)
+      hipLaunchKernelGGL((qproj_fast_kernel<8, true>), grid, dim3(256), 0, s, a);
+    else
+      return hipErrorInvalidValue;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    long long blocks = ((long long)a.M * (a.N / 4) + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(qproj_split_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   if (bits == 4)
-    hipLaunchKernelGGL(qproj_fast_kernel<4>, dim3(tiles), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((qproj_fast_kernel<4, false>), dim3(tiles), dim3(256), 0, s, a);
   else if (bits == 8)
-    hipLaunchKernelGGL(qproj_fast_kernel<8>, dim3(tiles), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((qproj_fast_kernel<8, false>), dim3(tiles), dim3(256), 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -948,8 +1027,11 @@ hipError_t launch_bf16_to_f16(const uint16_t* x, long long ldx, uint16_t* y,
 
 hipError_t validate_qproj_fast_kernels() {
   hipFuncAttributes fa;
-  const void* fns[] = {reinterpret_cast<const void*>(&qproj_fast_kernel<4>),
-                       reinterpret_cast<const void*>(&qproj_fast_kernel<8>),
+  const void* fns[] = {reinterpret_cast<const void*>(&qproj_fast_kernel<4, false>),
+                       reinterpret_cast<const void*>(&qproj_fast_kernel<8, false>),
+                       reinterpret_cast<const void*>(&qproj_fast_kernel<4, true>),
+                       reinterpret_cast<const void*>(&qproj_fast_kernel<8, true>),
+                       reinterpret_cast<const void*>(&qproj_split_reduce_kernel),
                        reinterpret_cast<const void*>(&repack_fast_kernel),
                        reinterpret_cast<const void*>(&repack_sbf_kernel),
                        reinterpret_cast<const void*>(&bf16_to_f16_kernel),

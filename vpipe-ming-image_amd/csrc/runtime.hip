@@ -966,6 +966,19 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       a.x = xh; a.ldx = K; a.codes = q->codes_f; a.sb = q->sbf;
       a.g = o.gate; a.ldg = o.ldg;     // the fast epilogue fuses SwiGLU
       a.yh = o.yh; a.ldyh = q->N;      // and writes the fp16 copy the next projection reads
+      // Few tiles (the context refiner's 256 caption rows: 15 or 40): split
+      // K so about one round of the chip runs, at least 6 K steps a slice
+      const int tiles = ((M + 255) / 256) * ((q->N + 255) / 256);
+      if (tiles < 64 && c->route == MING_ROUTE_AUTO && q->N % 4 == 0) {
+        int ks = 256 / tiles;
+        if (ks > (K / 64) / 6) ks = (K / 64) / 6;
+        if (ks >= 2) {
+          int rc = ensure_part(c, (size_t)ks * M * q->N * 4);
+          if (rc != MING_OK) return rc;
+          a.part = (float*)c->part;
+          a.kslices = ks;
+        }
+      }
     }
     const double base_flops = 2.0 * M * (double)q->N * K;
     const double wbytes = q->bits == 16
