@@ -249,7 +249,8 @@ int ming_bias_act(ming_ctx* ctx, uint16_t* y, int64_t ldy,
 /* y = bf16(silu(x)) over n elements. */
 int ming_silu(ming_ctx* ctx, const uint16_t* x, uint16_t* y, int n);
 /* The final layer's LayerNorm (no affine) then * (1 + scale[n])
- * (ming-dit.cc:2553-2563, eps 1e-6 there). */
+ * (ming-dit.cc:2553-2563, eps 1e-6 there). D % 8 == 0, D <= 8192, strides
+ * % 8 == 0, pointers 16-byte aligned. */
 int ming_ln_modulate(ming_ctx* ctx, const uint16_t* x, int64_t ldx,
                      const uint16_t* scale, uint16_t* y, int64_t ldy, int rows,
                      int D, float eps);

@@ -160,28 +160,69 @@ __global__ void bias_act_kernel(uint16_t* y, long long ldy, const uint16_t* b,
 
 // Final layer: LayerNorm (no affine, eps) then * (1 + scale[n]); one wave
 // per row, stats in f32.
+// One wave per row; the row is read once, 16 bytes per load, into registers
+// (chunk c = lane + 64 i of 8 elements, D <= 8192), then mean, the centered
+// variance and the output are taken from them.
 __global__ __launch_bounds__(256) void ln_modulate_kernel(
     const uint16_t* x, long long ldx, const uint16_t* scale, uint16_t* y,
     long long ldy, int rows, int D, float eps) {
+  constexpr int CPL = 16;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
+  const int nch = D >> 3;
   const uint16_t* xr = x + (long long)row * ldx;
+  uint4 v[CPL];
   float s = 0.0f;
-  for (int c = lane; c < D; c += 64) s += bf16_to_f32(xr[c]);
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nch) v[i] = *reinterpret_cast<const uint4*>(xr + 8 * c);
+  }
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    if (lane + 64 * i < nch) {
+      const uint32_t* u = &v[i].x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s += bf16_lo(u[e]) + bf16_hi(u[e]);
+    }
+  }
   s = warp_sum(s);
   const float mean = s / (float)D;
-  float v = 0.0f;
-  for (int c = lane; c < D; c += 64) {
-    const float d = bf16_to_f32(xr[c]) - mean;
-    v = fmaf(d, d, v);
+  float var = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    if (lane + 64 * i < nch) {
+      const uint32_t* u = &v[i].x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d0 = bf16_lo(u[e]) - mean, d1 = bf16_hi(u[e]) - mean;
+        var = fmaf(d0, d0, var);
+        var = fmaf(d1, d1, var);
+      }
+    }
   }
-  v = warp_sum(v);
-  const float inv = 1.0f / sqrtf(v / (float)D + eps);
+  var = warp_sum(var);
+  const float inv = 1.0f / sqrtf(var / (float)D + eps);
   uint16_t* yr = y + (long long)row * ldy;
-  for (int c = lane; c < D; c += 64) {
-    const float nrm = bf16_to_f32((uint16_t)f32_to_bf16_bits((bf16_to_f32(xr[c]) - mean) * inv));
-    yr[c] = (uint16_t)f32_to_bf16_bits(nrm * (1.0f + bf16_to_f32(scale[c])));
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      const uint4 sc = *reinterpret_cast<const uint4*>(scale + 8 * c);
+      const uint32_t* u = &v[i].x;
+      const uint32_t* su = &sc.x;
+      uint4 o;
+      uint32_t* ou = &o.x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t nb = pack_bf16x2_rne((bf16_lo(u[e]) - mean) * inv,
+                                            (bf16_hi(u[e]) - mean) * inv);
+        ou[e] = pack_bf16x2_rne(bf16_lo(nb) * (1.0f + bf16_lo(su[e])),
+                                bf16_hi(nb) * (1.0f + bf16_hi(su[e])));
+      }
+      *reinterpret_cast<uint4*>(yr + 8 * c) = o;
+    }
   }
 }
 

@@ -1428,6 +1428,11 @@ int ming_ln_modulate(ming_ctx* c, const uint16_t* x, int64_t ldx,
   int rc = elt_check(c, x, scale, rows, D);
   if (rc != MING_OK) return rc;
   if (!y) return fail(MING_ERR_ARG, "null argument");
+  // the kernel holds a row in registers, 16-byte chunks
+  if (D % 8 != 0 || D > 8192 || ldx < D || ldy < D || ldx % 8 != 0 || ldy % 8 != 0)
+    return fail(MING_ERR_SHAPE, "ming_ln_modulate: need D % 8 == 0, D <= 8192, strides % 8 == 0");
+  if (!aligned(x, 16) || !aligned(y, 16) || !aligned(scale, 16))
+    return fail(MING_ERR_ARG, "ming_ln_modulate: pointers must be 16-byte aligned");
   if (rows == 0) return ok();
   DeviceGuard dg(c->device);
   MING_HIP(profiled(c, kBLn, 0.0, 4.0 * rows * D,
