@@ -136,15 +136,18 @@ def forward_flops(img, cap, ranks=RANKS, scales=SCALES):
 
 
 def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2, bits=4,
-                        ranks=RANKS):
+                        ranks=RANKS, ref=None):
     """A 34-block w{bits}g64 model with random-init weights (quantized on the
     GPU by the library's pack writer), an adapter of each rank in `ranks`
     bound on all seven projections of every block (slot i = ranks[i]; the
     config-2 set by default), dense embedders and final layer. The model's
-    projection weights are listed in model.projections."""
+    projection weights are listed in model.projections. When `ref` is a
+    dict, it is filled with the same weights as device tensors in the layout
+    an fp32 reference of the forward reads (the tests' torch reference)."""
     dev = "cuda"
     keep = []
     projections = []
+    packs = {}
 
     def qw(N, K):
         w = torch.randn((N, K), generator=gen, device=dev) * 0.02
@@ -155,10 +158,13 @@ def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2, bits=4,
         ctx.quantize_pack(w, N, K, bits, codes, sc, bi)
         ctx.synchronize()
         q = m.QWeight.quantized(ctx, codes, sc, bi, bits, on_device=True)
+        if ref is not None:
+            packs[id(q)] = {"codes": codes, "scales": sc, "biases": bi, "bits": bits}
         return q
 
     def lora(q, N, K):
         projections.append(q)
+        kept = []
         for slot, r in enumerate(ranks):
             A = (torch.randn((r, K), generator=gen, device=dev) / K ** 0.5
                  ).to(torch.bfloat16).view(torch.int16)
@@ -166,6 +172,8 @@ def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2, bits=4,
                  ).to(torch.bfloat16).view(torch.int16)
             torch.cuda.synchronize()
             q.bind_lora(slot, A, B, on_device=True)
+            kept.append((A, B, 1.0))
+        return kept
 
     def vec(n, base, std):
         v = (base + std * torch.randn((n,), generator=gen, device=dev))
@@ -177,16 +185,20 @@ def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2, bits=4,
         w = (torch.randn((N, K), generator=gen, device=dev) / K ** 0.5
              ).to(torch.bfloat16).view(torch.int16).contiguous()
         torch.cuda.synchronize()
-        return m.QWeight.dense(ctx, w, on_device=True)
+        q = m.QWeight.dense(ctx, w, on_device=True)
+        if ref is not None:
+            packs[id(q)] = {"w": w}
+        return q
 
     def block(modulated):
         parts = {}
+        rb = {"loras": {}}
         for name, (N, K) in {"q": (HID, HID), "k": (HID, HID),
                              "v": (HID, HID), "o": (HID, HID),
                              "w1": (FFN, HID), "w3": (FFN, HID),
                              "w2": (HID, FFN)}.items():
             parts[name] = qw(N, K)
-            lora(parts[name], N, K)
+            rb["loras"][name] = lora(parts[name], N, K)
         if modulated:
             parts["ada"] = qw(4 * HID, 256)
             parts["ada_b"] = vec(4 * HID, 0.0, 0.1)
@@ -194,8 +206,16 @@ def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2, bits=4,
             parts[g] = vec(HID, 1.0, 0.1)
         parts["nq"] = vec(128, 1.0, 0.1)
         parts["nk"] = vec(128, 1.0, 0.1)
+        if ref is not None:
+            for k, v in parts.items():
+                rb[k] = packs.pop(id(v)) if isinstance(v, m.QWeight) else v
+            (ref["blocks"] if modulated else ref["ctx_blocks"]).append(rb)
         return m.block_desc(**parts)
 
+    if ref is not None:
+        ref.update({"hidden": HID, "n_heads": 30, "n_refiner": n_refiner, "cap_dim": 2560,
+                    "time_freq": 256, "t_scale": 1000.0, "eps": 1e-5,
+                    "ctx_blocks": [], "blocks": []})
     cb, mb = [], []
     for i in range(2 * n_refiner + n_layers):
         (cb if i < n_refiner else mb).append(block(i >= n_refiner))
@@ -217,6 +237,8 @@ def build_forward_model(ctx, m, torch, gen, n_layers=30, n_refiner=2, bits=4,
           "final_lin_b": vec(64, 0.0, 0.05)}
     for k, v in tw.items():
         setattr(d, k, m._h(v))
+        if ref is not None:
+            ref[k] = packs.pop(id(v)) if isinstance(v, m.QWeight) else v
     model = m.Model(ctx, d, cb, mb, keep=keep + [tw, cb, mb])
     model.projections = projections
     return model

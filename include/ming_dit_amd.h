@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MING_ABI_VERSION 3
+#define MING_ABI_VERSION 4
 
 /* Runtime-LoRA slots: lora::Stack::kMax (ming-dit.h:117) and the eight
  * `lora`..`lora8` keys (ming-model-config-stage.h:37-56). */
@@ -65,6 +65,9 @@ typedef struct ming_engagement {
   int64_t gemm_fast;    /* of the quantized projections, those on the fast route */
   int64_t cap_cache_hits; /* forwards whose caption path came from the caption cache */
   int64_t gemv;           /* of the projections, those run as a GEMV (M <= 8, no live adapter) */
+  int64_t gemm_split;     /* of the fast-route projections, those split along K (< 64 tiles) */
+  int64_t range_faults;   /* synchronizations that found a saturated fp16 input copy
+                             (MING_ERR_RANGE; see MING_ROUTE_WIDE) */
 } ming_engagement;
 
 /* Kernel routes for quantized projections. AUTO takes the fast route

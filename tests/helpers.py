@@ -86,33 +86,42 @@ def build_block(ctx, seed, H, F, adaln, bits=4, modulated=True,
     quantized by the oracle's packer; gains ~ 1 + N(0, .1); adaLN bias
     ~ N(0, .1); LoRA (slot, rank, fold) bound on all seven projections. Every
     tensor has a fixed seed of its own, so the same seed with other slots
-    gives the same base block."""
-    import ming_dit_amd as m
+    gives the same base block. With ctx None only the oracle dict is made
+    (gp and the desc are None)."""
+    gpu = ctx is not None
+    if gpu:
+        import ming_dit_amd as m
     ob = {"loras": {}}
     gp = {}
     for i, (name, (N, K)) in enumerate(block_proj_shapes(H, F).items()):
         pack, _ = make_weight(seed + 100 * i, N, K, bits)
         ob[name] = dict(pack, bits=bits)
         qw = m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
-                                 pack["biases"], bits)
+                                 pack["biases"], bits) if gpu else None
         lor = [None] * 8
         for slot, rank, fold in slots:
             A, B = make_lora(seed + 100 * i + 10 + 2 * slot, N, K, rank)
-            qw.bind_lora(slot, A, B, fold)
+            if gpu:
+                qw.bind_lora(slot, A, B, fold)
             lor[slot] = (A, B, fold)
         ob["loras"][name] = lor
         gp[name] = qw
     if modulated:
         pack, _ = make_weight(seed + 1000, 4 * H, adaln, bits)
         ob["ada"] = dict(pack, bits=bits)
-        gp["ada"] = m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
-                                        pack["biases"], bits)
+        if gpu:
+            gp["ada"] = m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
+                                            pack["biases"], bits)
         ob["ada_b"] = bf16(randn(seed + 1001, (4 * H,), 0.1))
-        gp["ada_b"] = to_dev(ob["ada_b"])
+        if gpu:
+            gp["ada_b"] = to_dev(ob["ada_b"])
     for j, (g, n) in enumerate((("an1", H), ("an2", H), ("fn1", H),
                                 ("fn2", H), ("nq", 128), ("nk", 128))):
         ob[g] = bf16(1.0 + randn(seed + 1002 + j, (n,), 0.1))
-        gp[g] = to_dev(ob[g])
+        if gpu:
+            gp[g] = to_dev(ob[g])
+    if not gpu:
+        return ob, None, None
     return ob, gp, m.block_desc(**gp)
 
 
@@ -127,8 +136,11 @@ def build_model(ctx, seed, H=256, NH=2, F=512, n_layers=2, n_refiner=1,
                 cap_dim=128, bits=4, slots=((0, 4, 1.0), (3, 16, 0.5))):
     """A random model: (oracle dict for oracle.model_forward, Model). The
     non-block weights are dense bf16, as the reference leaves them
-    (MingQuantFamily excludes the embedders and the final layer)."""
-    import ming_dit_amd as m
+    (MingQuantFamily excludes the embedders and the final layer). With ctx
+    None only the oracle dict is made (the Model is None)."""
+    gpu = ctx is not None
+    if gpu:
+        import ming_dit_amd as m
     mo = {"hidden": H, "n_heads": NH, "n_refiner": n_refiner,
           "cap_dim": cap_dim, "time_freq": time_freq, "t_scale": 1000.0,
           "rope_theta": 256.0, "axes": (32, 48, 48), "eps": 1e-5}
@@ -156,11 +168,14 @@ def build_model(ctx, seed, H=256, NH=2, F=512, n_layers=2, n_refiner=1,
                                       ("final_lin", patch_dim, H))):
         pack, _ = make_weight(seed + 500 + 2 * j, N, K, 16, std=1.0 / np.sqrt(K))
         mo[name] = pack
-        dev[name] = m.QWeight.dense(ctx, pack["w"])
         b = bf16(randn(seed + 501 + 2 * j, (N,), 0.05))
         mo[name + "b" if name.startswith("time") else name + "_b"] = b
-        dev[name + "b" if name.startswith("time") else name + "_b"] = to_dev(b)
+        if gpu:
+            dev[name] = m.QWeight.dense(ctx, pack["w"])
+            dev[name + "b" if name.startswith("time") else name + "_b"] = to_dev(b)
     mo["cap_norm"] = bf16(1.0 + randn(seed + 600, (cap_dim,), 0.1))
+    if not gpu:
+        return mo, None
     dev["cap_norm"] = to_dev(mo["cap_norm"])
     d = m.ModelDesc()
     d.hidden, d.n_heads, d.ffn, d.n_layers, d.n_refiner = H, NH, F, n_layers, n_refiner

@@ -18,7 +18,16 @@ def test_library_exports_every_header_symbol():
 
 
 def test_abi_version():
-    assert m.lib().ming_abi_version() == 3
+    assert m.lib().ming_abi_version() == 4
+
+
+def test_engagement_layout_matches_the_header():
+    """The ctypes mirror of ming_engagement has the header's fields in order."""
+    import re
+    txt = open(m.HEADER).read()
+    body = txt[txt.index("typedef struct ming_engagement"):txt.index("} ming_engagement;")]
+    names = re.findall(r"int64_t\s+(\w+);", body)
+    assert names == [n for n, _ in m.Engagement._fields_]
 
 
 def test_null_arguments_are_refused_with_a_reason():

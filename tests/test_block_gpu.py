@@ -109,12 +109,18 @@ def test_block_rejects_bad_desc(ctx):
 
 def test_block_config3_full_size(ctx):
     """Config 3: H 3840, 30 heads, ffn 10240, 4352 rows, w4g64, the config-2
-    adapter set on all seven projections. Finite, deterministic, and all
+    adapter set on all seven projections. Against the fp32 reference
+    (tests/torch_ref.py, pinned to the oracle at reduced width) by the
+    reference's own rule for full-size checks (ming-dit-test.cc:2131): within
+    twice the distance of a bf16 run from f32, floored at the reduced-width
+    bars (output 1e-2, update 2e-2). Then finite, deterministic, and all
     strengths 0 equal to the unadapted block bit for bit."""
     import torch
     import ming_dit_amd as m
+    import torch_ref as tr
     Hf, NHf, Ff, ADAf, rows = 3840, 30, 10240, 256, 4352
     gen = torch.Generator(device="cuda").manual_seed(3)
+    packs = {}
 
     def qw(N, K):
         w = torch.randn((N, K), generator=gen, device="cuda") * 0.02
@@ -124,7 +130,9 @@ def test_block_config3_full_size(ctx):
         torch.cuda.synchronize()
         ctx.quantize_pack(w, N, K, 4, codes, sc, bi)
         ctx.synchronize()
-        return m.QWeight.quantized(ctx, codes, sc, bi, 4, on_device=True)
+        q = m.QWeight.quantized(ctx, codes, sc, bi, 4, on_device=True)
+        packs[id(q)] = {"codes": codes, "scales": sc, "biases": bi, "bits": 4}
+        return q
 
     def vec(n, base=1.0, std=0.1):
         v = base + std * torch.randn((n,), generator=gen, device="cuda")
@@ -133,6 +141,7 @@ def test_block_config3_full_size(ctx):
     shapes = {"q": (Hf, Hf), "k": (Hf, Hf), "v": (Hf, Hf), "o": (Hf, Hf),
               "w1": (Ff, Hf), "w3": (Ff, Hf), "w2": (Hf, Ff)}
     parts = {n: qw(*sh) for n, sh in shapes.items()}
+    ref_blk = {"loras": {n: [] for n in shapes}}
     for n, (N, K) in shapes.items():
         for slot, r in enumerate(CFG2_RANKS):
             A = (torch.randn((r, K), generator=gen, device="cuda") / K ** 0.5
@@ -141,6 +150,7 @@ def test_block_config3_full_size(ctx):
                  ).to(torch.bfloat16).view(torch.int16)
             torch.cuda.synchronize()
             parts[n].bind_lora(slot, A, B, 1.0, on_device=True)
+            ref_blk["loras"][n].append((A, B, 1.0))
     ada = qw(4 * Hf, ADAf)
     gains = dict(ada_b=vec(4 * Hf, 0.0, 0.1), an1=vec(Hf), an2=vec(Hf),
                  fn1=vec(Hf), fn2=vec(Hf), nq=vec(128), nk=vec(128))
@@ -150,7 +160,12 @@ def test_block_config3_full_size(ctx):
           ).to(torch.bfloat16).view(torch.int16)
     temb = (torch.randn((ADAf,), generator=gen, device="cuda")
             ).to(torch.bfloat16).view(torch.int16)
-    pt, ph, pw = grid_positions(rows, 64)
+    # config 3's positions: the 64 x 64 patch grid at (257, h, w), then the
+    # 256 text rows at (1 + i, 0, 0)
+    img, cap = 4096, 256
+    pt = np.concatenate([np.full(img, cap + 1), 1 + np.arange(cap)]).astype(np.int32)
+    ph = np.concatenate([np.arange(img) // 64, np.zeros(cap)]).astype(np.int32)
+    pw = np.concatenate([np.arange(img) % 64, np.zeros(cap)]).astype(np.int32)
     c, s = orc.rope_table(pt, ph, pw)
     cd, sd = to_dev(c), to_dev(s)
     ws = torch.empty(ctx.block_workspace_bytes(d, rows), dtype=torch.uint8,
@@ -166,6 +181,26 @@ def test_block_config3_full_size(ctx):
     a = run(desc, CFG2_SCALES)
     assert np.all(np.isfinite(f32(a)))
     assert not np.array_equal(a, from_dev(x0))
+    # the fp32 reference, and the bf16 run that sets the bar
+    ref_blk.update({n: packs[id(q)] for n, q in dict(parts, ada=ada).items()})
+    ref_blk.update(gains)
+    x0f = tr.bf(x0, "cuda")
+    ct, st = torch.from_numpy(c).cuda(), torch.from_numpy(s).cuda()
+    tt = tr.bf(temb, "cuda")
+    outs = {}
+    for mode in ("f32", "bf16"):
+        outs[mode] = tr.Ref(mode, "cuda").block(x0f, ref_blk, NHf, ct, st, tt, CFG2_SCALES)
+        torch.cuda.synchronize()
+    got = torch.from_numpy(f32(a)).cuda()
+    rel = tr.rel_l2(got, outs["f32"])
+    upd = tr.rel_l2(got - x0f, outs["f32"] - x0f)
+    bar_out = max(1e-2, 2 * tr.rel_l2(outs["bf16"], outs["f32"]))
+    bar_upd = max(2e-2, 2 * tr.rel_l2(outs["bf16"] - x0f, outs["f32"] - x0f))
+    print(f"configs[2] block vs fp32: output {rel:.3e} (bar {bar_out:.3e}), update "
+          f"{upd:.3e} (bar {bar_upd:.3e}); vs the bf16 run: update "
+          f"{tr.rel_l2(got - x0f, outs['bf16'] - x0f):.3e}", flush=True)
+    assert rel <= bar_out and upd <= bar_upd
+    del outs, got
     assert np.array_equal(a, run(desc, CFG2_SCALES))
     z = run(desc, [0.0] * 8)
     assert not np.array_equal(a, z)

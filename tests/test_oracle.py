@@ -289,11 +289,24 @@ def test_rmsnorm_power_of_two_invariance(orc):
                        atol=4e-3)
 
 
-def test_fold_gain(orc):
+def test_fold_gain_special_cases(orc):
+    """nw = norm_w * (1 + scale) (ming-dit.cc:2266-2273): scale 0 is the
+    identity, -1 the zero gain, 1 and 3 the exact doublings; a dropped "1 +",
+    a swapped operand or an added shift fails one of them."""
     nw = bf16(randn(43, (64,)))
-    sc = bf16(randn(44, (64,), 0.1))
-    assert np.array_equal(orc.fold_gain(nw, sc),
-                          bf16(f32(nw) * (1.0 + f32(sc))))
+    z = bf16(np.zeros(64, np.float32))
+    assert np.array_equal(orc.fold_gain(nw, z), nw)
+    assert np.all(f32(orc.fold_gain(nw, bf16(np.full(64, -1.0, np.float32)))) == 0.0)
+    assert np.array_equal(orc.fold_gain(nw, bf16(np.ones(64, np.float32))), bf16(2 * f32(nw)))
+    assert np.array_equal(orc.fold_gain(nw, bf16(np.full(64, 3.0, np.float32))),
+                          bf16(4 * f32(nw)))
+    # a per-element scale: one rounding of the f32 product (torch's bf16
+    # multiply of exact operands: 1 + s is exact for these s); the fold adds
+    # a zero shift, so a -0 product reads +0 (values compared)
+    sc = bf16(np.round(randn(44, (64,)) * 8) / 8)
+    want = (torch.from_numpy(f32(nw)).to(torch.bfloat16)
+            * (1.0 + torch.from_numpy(f32(sc))).to(torch.bfloat16))
+    assert np.array_equal(f32(orc.fold_gain(nw, sc)), want.float().numpy())
 
 
 # ---- rotary -------------------------------------------------------------------------------
@@ -382,15 +395,119 @@ def test_attention_special_cases(orc):
     assert np.allclose(o, f32(v2).mean(0, keepdims=True), atol=2e-2)
 
 
-def test_swiglu_and_gated_residual(orc):
-    g = bf16(randn(80, (4, 64)))
-    u = bf16(randn(81, (4, 64)))
-    gf, uf = f32(g), f32(u)
-    assert np.array_equal(orc.swiglu(g, u),
-                          bf16((gf / (1 + np.exp(-gf))).astype(np.float32) * uf))
-    h = bf16(randn(82, (4, 64)))
-    gate = bf16(randn(83, (64,)))
-    want = bf16(f32(h) + np.tanh(f32(gate)).astype(np.float32) * f32(u))
-    got = orc.gated_residual(h, gate, u)
-    # tanhf vs numpy's tanh may differ in the last f32 ulp: allow 1 bf16 ulp
-    assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1
+def _ulps(a, b):
+    """bf16 distance in units of the last place (sign-aware, -0 == +0)."""
+    def key(u):
+        v = np.asarray(u, np.uint16).astype(np.int32)
+        return np.where(v >= 0x8000, -(v & 0x7FFF), v)
+    return np.abs(key(a) - key(b))
+
+
+def _t(a):
+    """bf16 bit patterns -> a float64 torch tensor of their values."""
+    return torch.from_numpy(f32(a).astype(np.float64))
+
+
+def _tb(t):
+    """A float torch tensor -> bf16 bit patterns by torch's own cast."""
+    return t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_swiglu_against_torch_silu(orc):
+    """silu(g) * u rounded once (ming_ops.metal:97-112) against torch's
+    F.silu in float64: within one bf16 ulp (f32 expf against f64), and
+    the zero and saturation cases exactly."""
+    g = bf16(randn(80, (16, 256)) * 3)
+    u = bf16(randn(81, (16, 256)))
+    got = orc.swiglu(g, u)
+    want = _tb(torch.nn.functional.silu(_t(g)) * _t(u))
+    d = _ulps(got, want)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    # silu(0) = 0; u = 0 gives 0; silu(g) -> g for large g, -> 0 for very negative g
+    assert np.all(f32(orc.swiglu(bf16(np.zeros(64, np.float32)), u[0, :64])) == 0)
+    assert np.all(f32(orc.swiglu(g[0, :64], bf16(np.zeros(64, np.float32)))) == 0)
+    big = bf16(np.full(8, 40.0, np.float32))
+    one = bf16(np.ones(8, np.float32))
+    assert np.array_equal(orc.swiglu(big, one), big)
+    assert np.all(np.abs(f32(orc.swiglu(bf16(np.full(8, -40.0, np.float32)), one))) < 1e-15)
+
+
+def test_gated_residual_against_torch_tanh(orc):
+    """h + tanh(gate) * sub rounded once (ming_ops.metal:59-74) against torch's
+    tanh in float64; gate 0 leaves h; a gate of +-inf adds +-sub once."""
+    h = bf16(randn(82, (8, 128)))
+    sub = bf16(randn(81, (8, 128)))
+    gate = bf16(randn(83, (128,)))
+    got = orc.gated_residual(h, gate, sub)
+    want = _tb(_t(h) + torch.tanh(_t(gate))[None, :] * _t(sub))
+    d = _ulps(got, want)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    assert np.array_equal(orc.gated_residual(h, bf16(np.zeros(128, np.float32)), sub), h)
+    inf = bf16(np.full(128, np.inf, np.float32))
+    assert np.array_equal(orc.gated_residual(h, inf, sub), orc.residual_add(h, sub))
+
+
+def test_residual_add_is_torch_bf16_add(orc):
+    """h + sub rounded once (ming_ops.metal:43-52) is torch's bf16 add (f32 sum,
+    round to nearest even) bit for bit; h + (-h) = 0 and h + 0 = h."""
+    h = bf16(randn(84, (32, 384)) * 4)
+    sub = bf16(randn(85, (32, 384)))
+    got = orc.residual_add(h, sub)
+    th = torch.from_numpy(h.view(np.int16)).view(torch.bfloat16)
+    ts = torch.from_numpy(sub.view(np.int16)).view(torch.bfloat16)
+    assert np.array_equal(got, (th + ts).view(torch.int16).numpy().view(np.uint16))
+    assert np.all(f32(orc.residual_add(h, bf16(-f32(h)))) == 0)
+    assert np.array_equal(orc.residual_add(h, bf16(np.zeros_like(f32(h)))), h)
+
+
+def test_bias_act_and_silu_against_torch(orc):
+    """The timestep MLP's bias (+ SiLU) (ming-dit.cc:2276-2281): the bias add
+    is torch's bf16 add bit for bit; SiLU of that bf16 sum is torch's F.silu
+    in float64 within one bf16 ulp; silu_bf16 is the same with a zero bias."""
+    y = bf16(randn(86, (4, 1024)) * 2)
+    b = bf16(randn(87, (1024,)) * 0.5)
+    ty = torch.from_numpy(y.view(np.int16)).view(torch.bfloat16)
+    tb = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
+    s = ty + tb[None, :]
+    assert np.array_equal(orc.bias_act(y, b), s.view(torch.int16).numpy().view(np.uint16))
+    got = orc.bias_act(y, b, silu=True)
+    want = _tb(torch.nn.functional.silu(s.double()))
+    d = _ulps(got, want)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    d = _ulps(orc.silu_bf16(y), _tb(torch.nn.functional.silu(_t(y))))
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    special = bf16(np.array([0.0, 40.0, -40.0, 1.0], np.float32))
+    sv = f32(orc.silu_bf16(special))
+    assert sv[0] == 0 and sv[1] == 40.0 and -1e-15 < sv[2] <= 0
+    assert sv[3] == f32(bf16(np.float32(1.0 / (1.0 + np.exp(-1.0)))))
+
+
+def test_ln_modulate_against_torch_layer_norm(orc):
+    """The final layer's LayerNorm without affine (eps 1e-6), rounded to bf16,
+    then * (1 + scale) (ming-dit.cc:2553-2563): with scale 0, torch's
+    layer_norm in float64 within one ulp on rows of non-zero mean and spread,
+    each row zero-mean and unit-variance; a row whose variance is far below
+    eps (the eps placement decides it); scale -1 gives 0, scale 1 doubles."""
+    D = 3840
+    mu = np.array([0.0, 3.0, -7.5, 100.0], np.float32)[:, None]
+    sd = np.array([1.0, 0.25, 4.0, 2.0], np.float32)[:, None]
+    x = bf16(randn(88, (4, D)) * sd + mu)
+    tiny = bf16(randn(89, (1, D)) * 1e-4)       # variance 1e-8 << eps
+    x = np.concatenate([x, tiny])
+    zero = bf16(np.zeros(D, np.float32))
+    y0 = orc.ln_modulate(x, zero, eps=1e-6)
+    want = _tb(torch.nn.functional.layer_norm(_t(x), (D,), eps=1e-6))
+    d = _ulps(y0, want)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    yf = f32(y0[:4]).astype(np.float64)
+    assert np.all(np.abs(yf.mean(-1)) < 1e-2) and np.all(np.abs(yf.var(-1) - 1) < 1e-2)
+    # the tiny row is scaled by 1/sqrt(var + eps) ~ 995, not 1/sqrt(var) ~ 1e4
+    assert 0.05 < np.sqrt((f32(y0[4]).astype(np.float64) ** 2).mean()) < 0.15
+    # at D = 16 the n vs n - 1 variance differs by 3% (~8 ulps): torch's is n
+    xs = bf16(randn(90, (64, 16)) * 2 + 1)
+    d = _ulps(orc.ln_modulate(xs, zero[:16], eps=1e-6),
+              _tb(torch.nn.functional.layer_norm(_t(xs), (16,), eps=1e-6)))
+    assert d.max() <= 1
+    assert np.all(f32(orc.ln_modulate(x, bf16(np.full(D, -1.0, np.float32)), eps=1e-6)) == 0)
+    assert np.array_equal(orc.ln_modulate(x, bf16(np.ones(D, np.float32)), eps=1e-6),
+                          bf16(2 * f32(y0)))

@@ -71,9 +71,12 @@ def test_base_projection_parity(ctx, orc, bits, M, N, K):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-def test_lora_eight_slots_parity(ctx, orc, bits):
-    """BASELINE config 2's adapter set on one projection."""
-    M, N, K = 320, 768, 1024
+@pytest.mark.parametrize("M,N,K", [(320, 768, 1024), (520, 8192, 512)])
+def test_lora_eight_slots_parity(ctx, orc, bits, M, N, K):
+    """BASELINE config 2's adapter set on one projection (a 9-chunk LoRA
+    tail): on a few tiles (6: the fast route splits K) and on a grid of 96
+    tiles with a ragged last tile-row (the unsplit fast kernel)."""
+    print(f"case eight slots bits={bits} M={M} N={N} K={K}", flush=True)
     x = bf16(randn(11, (M, K)))
     pack, w = make_weight(12, N, K, bits)
     qw = _qw(ctx, pack, bits)
@@ -87,6 +90,9 @@ def test_lora_eight_slots_parity(ctx, orc, bits):
     y = _run(ctx, qw, to_dev(x), M, CFG2_SCALES)
     eng = ctx.engagement()
     assert eng["lora_proj"] == 1 and eng["lora_xa"] == 1
+    tiles = ((M + 255) // 256) * ((N + 255) // 256)
+    assert eng["gemm_fast"] == (1 if route_is_auto(ctx) else 0)
+    assert eng["gemm_split"] == (1 if route_is_auto(ctx) and tiles < 64 else 0)
     ref = orc.proj(x, w, loras)
     base = orc.proj(x, w)
     rel = _rel(orc, y, ref)
@@ -388,6 +394,7 @@ def test_few_tiles_split_k_parity(ctx, orc, bits):
     y = _run(ctx, qw, to_dev(x), M, CFG2_SCALES)
     eng = ctx.engagement()
     assert eng["lora_proj"] == 1 and eng["gemm_fast"] == (1 if route_is_auto(ctx) else 0)
+    assert eng["gemm_split"] == eng["gemm_fast"]
     ref = orc.proj(x, w, loras)
     assert _rel(orc, y, ref) <= TOL
     assert orc.rel_l2(ref, orc.proj(x, w)) > 10 * TOL
@@ -419,3 +426,79 @@ def test_few_tiles_ffn_equals_the_four_calls(ctx):
 
 def orc_f32(v):
     return (v.astype(np.uint32) << 16).view(np.float32)
+
+
+def _cfg2_rows(M, tile=256):
+    """A row sample covering every 256-row M tile: its first and last row
+    and one interior row that moves from tile to tile."""
+    rows = []
+    for t in range((M + tile - 1) // tile):
+        lo, hi = t * tile, min(M, (t + 1) * tile) - 1
+        rows += [lo, min(hi, lo + 1 + (37 * t) % (tile - 2)), hi]
+    return np.array(sorted(set(rows)), np.int64)
+
+
+def test_config2_ffn_full_size(ctx, orc):
+    """BASELINE configs[1] exactly: X [4352, 3840] ~ N(0, 1) bf16, w1/w3
+    3840 -> 10240 and w2 10240 -> 3840 as w4g64 packs of N(0, 0.02) weights,
+    the eight slots {4, 8, 16, 16, 32, 32, 64, 128} at strengths
+    {1, .5, 0, -.3, .8, 0, 1.2, .25} on all three, through ming_ffn (the
+    bench's step). 17 x 40 = 680 tiles: the unsplit w4 kernel with the
+    9-chunk tail and, on w3, the fused SwiGLU epilogue. On a row sample over
+    all 17 M tiles, against the oracle (gpu_ff, ming-dit.cc:2151-2162):
+      h (w3's fused epilogue) vs swiglu(bf16(x.W1'), bf16(x.W3')), and
+      y vs the f32 reference of w2 on the kernel's own h and on the
+      oracle's h, each to the projection bar."""
+    M, H, F = 4352, 3840, 10240
+    x = bf16(randn(2001, (M, H)))
+    packs, loras = [], []
+    for i, (N, K) in enumerate(((F, H), (F, H), (H, F))):
+        codes, sc, bi = orc.quantize(randn(2010 + i, (N, K), 0.02), 4)
+        packs.append((codes, sc, bi))
+        lo = []
+        for s, r in enumerate(CFG2_RANKS):
+            A = bf16(randn(2100 + 20 * i + 2 * s, (r, K), 1.0 / np.sqrt(K)))
+            B = bf16(randn(2101 + 20 * i + 2 * s, (N, r), 0.01))
+            lo.append((A, B, CFG2_SCALES[s]))
+        loras.append(lo)
+    ws = []
+    for (codes, sc, bi), lo in zip(packs, loras):
+        qw = m.QWeight.quantized(ctx, codes, sc, bi, 4)
+        for s, (A, B, _) in enumerate(lo):
+            qw.bind_lora(s, A, B)
+        ws.append(qw)
+    xd = to_dev(x)
+    y = empty_bf16(M, H)
+    h = empty_bf16(M, F)
+    sync()
+    ctx.reset_engagement()
+    ctx.ffn(ws[0], ws[1], ws[2], xd, y, M, CFG2_SCALES, h=h)
+    sync()
+    eng = ctx.engagement()
+    auto = route_is_auto(ctx)
+    assert eng["gemm_q4"] == 3 and eng["lora_proj"] == 3 and eng["lora_xa"] == 2
+    assert eng["gemm_fast"] == (3 if auto else 0) and eng["gemm_split"] == 0
+    rows = _cfg2_rows(M)
+    assert len(rows) == 51 and rows[-1] == M - 1
+    yh, hh = from_dev(y)[rows], from_dev(h)[rows]
+    xs = np.ascontiguousarray(x[rows])
+
+    def qp(inp, i):
+        codes, sc, bi = packs[i]
+        return orc.qproj_packed(np.ascontiguousarray(inp), codes, sc, bi, 4, loras[i])
+
+    g = qp(xs, 0)
+    u = qp(xs, 1)
+    h_ref = orc.swiglu(orc.f32_to_bf16(g), orc.f32_to_bf16(u))
+    rel_h = orc.rel_l2(orc.bf16_to_f32(hh), orc.bf16_to_f32(h_ref))
+    rel_y_own = _rel(orc, yh, qp(hh, 2))
+    rel_y = _rel(orc, yh, qp(h_ref, 2))
+    base = orc.qproj_packed(xs, *packs[0], 4)
+    moved = orc.rel_l2(g, base)
+    print(f"configs[1] ffn ({'auto' if auto else 'general'}): h rel-L2 {rel_h:.3e}, "
+          f"y vs w2(own h) {rel_y_own:.3e}, y vs oracle chain {rel_y:.3e}, "
+          f"adapters move w1 by {moved:.3e}", flush=True)
+    assert rel_h <= TOL and rel_y_own <= TOL and rel_y <= TOL
+    assert moved > 10 * TOL
+    for w in ws:
+        w.close()

@@ -1033,6 +1033,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     if (o.gate) c->eng.elementwise += 1;
     if (o.took_fast) *o.took_fast = fast[i];
     if (fast[i]) c->eng.gemm_fast += 1;
+    if (fast[i] && a.kslices >= 2) c->eng.gemm_split += 1;
     if (q->bits == 4) c->eng.gemm_q4 += 1;
     else if (q->bits == 8) c->eng.gemm_q8 += 1;
     else c->eng.gemm_dense += 1;

@@ -8,18 +8,59 @@ built, importing it raises.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
+import sys
 import weakref
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-# MING_DIT_AMD_LIB points at another build of the same library (A/B runs).
-LIB_PATH = os.environ.get("MING_DIT_AMD_LIB",
-                          os.path.join(_HERE, "libming_dit_amd.so"))
+LIB_PATH = os.path.join(_HERE, "libming_dit_amd.so")
 HEADER = os.path.join(os.path.dirname(_HERE), "include", "ming_dit_amd.h")
 MAX_SLOTS = 8
 
 _lib = None
+
+# Every open handle, so that the ones still open when the interpreter exits
+# are closed by an atexit hook -- before module teardown and before the HIP
+# runtime's own exit handlers -- and never by a finalizer running during
+# interpreter shutdown, when the runtime may already be gone.
+_open = weakref.WeakSet()
+_atexit_registered = False
+
+
+def _track(obj):
+    global _atexit_registered
+    _open.add(obj)
+    if not _atexit_registered:
+        atexit.register(close_all)
+        _atexit_registered = True
+
+
+def close_all():
+    """Closes every handle still open: models before the weights they borrow,
+    weights before their contexts. Registered with atexit when the first
+    handle opens; safe to call at any time."""
+    objs = list(_open)
+    for kind in (Model, QWeight, Pack, Ctx):
+        for o in objs:
+            if isinstance(o, kind):
+                try:
+                    o.close()
+                except Exception:
+                    pass
+
+
+def _finalize(obj):
+    """__del__ body: close, unless the interpreter is shutting down (then the
+    atexit hook has closed what was open, and a late call into the HIP
+    runtime could run after its teardown)."""
+    if sys.is_finalizing():
+        return
+    try:
+        obj.close()
+    except Exception:
+        pass
 
 
 class MingError(RuntimeError):
@@ -35,7 +76,8 @@ class Engagement(C.Structure):
                 ("qk_norm_rope", C.c_int64), ("rope_table", C.c_int64),
                 ("attention", C.c_int64), ("elementwise", C.c_int64),
                 ("gemm_flops", C.c_uint64), ("gemm_fast", C.c_int64),
-                ("cap_cache_hits", C.c_int64), ("gemv", C.c_int64)]
+                ("cap_cache_hits", C.c_int64), ("gemv", C.c_int64),
+                ("gemm_split", C.c_int64), ("range_faults", C.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -258,6 +300,7 @@ class Ctx:
         _check(lib().ming_ctx_create(device, stream, C.byref(h)))
         self.h = h
         self._weights = weakref.WeakSet()
+        _track(self)
 
     def close(self):
         """Destroys the context's live weights first (the C-ABI refuses a
@@ -269,10 +312,7 @@ class Ctx:
             self.h = None
 
     def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+        _finalize(self)
 
     def set_stream(self, stream: int | None):
         _check(lib().ming_ctx_set_stream(self.h, stream))
@@ -427,6 +467,7 @@ class QWeight:
         self.ctx = ctx
         self.h = h
         ctx._weights.add(self)
+        _track(self)
         N, K, S = C.c_int(), C.c_int(), C.c_int()
         _check(lib().ming_qweight_shape(h, C.byref(N), C.byref(K),
                                         C.byref(S)))
@@ -480,10 +521,7 @@ class QWeight:
             self.h = None
 
     def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+        _finalize(self)
 
 
 def _h(obj) -> int | None:
@@ -549,6 +587,7 @@ class Pack:
         h = C.c_void_p()
         _check(lib().ming_pack_open(os.fsencode(transformer_dir), C.byref(h)))
         self.h = h
+        _track(self)
 
     def config(self) -> dict:
         c = DitConfig()
@@ -589,10 +628,7 @@ class Pack:
             self.h = None
 
     def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+        _finalize(self)
 
 
 def pack_write(src_dir: str, dst_dir: str, bits: int, threads: int = 0):
@@ -628,6 +664,7 @@ class Model:
             _check(lib().ming_model_create(ctx.h, C.byref(desc), C.byref(h)))
             self.h = h
         ctx._weights.add(self)
+        _track(self)
 
     @classmethod
     def load(cls, ctx: Ctx, transformer_dir: str, loras=None) -> "Model":
@@ -727,10 +764,7 @@ class Model:
             self.h = None
 
     def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+        _finalize(self)
 
 
 def header_symbols(path: str = HEADER):
