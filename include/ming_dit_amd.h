@@ -40,6 +40,8 @@ enum {
   MING_ERR_ALLOC = 4,   /* device memory could not be allocated */
   MING_ERR_KERNEL = 5,  /* a kernel failed validation at context creation */
   MING_ERR_STATE = 6,   /* the call does not fit the object's state */
+  MING_ERR_RANGE = 7,   /* a projection input on an fp16 route was >= 65536 in
+                           magnitude or not finite (see MING_ROUTE_WIDE) */
   MING_STOPPED = -1     /* a cooperative stop: not an error */
 };
 
@@ -75,8 +77,14 @@ typedef struct ming_engagement {
  * weight's scales and biases are exact in fp16, and a GEMV (each weight
  * streamed once, f32 dot products) for M <= 8 rows with no live adapter, as
  * the adaLN and timestep projections run at M = 1. GENERAL always takes the
- * general kernel. All compute the same function to the same bar. */
-enum { MING_ROUTE_AUTO = 0, MING_ROUTE_GENERAL = 1 };
+ * general kernel. Both multiply fp16 activations (bf16 values carried
+ * exactly below 2^16 in magnitude); a value of 2^16 or more, inf or NaN
+ * cannot be carried, and the next ming_ctx_synchronize (or the forward that
+ * met it) returns MING_ERR_RANGE instead of results. WIDE multiplies the
+ * bf16 activations themselves with each dequantized weight split into a
+ * bf16 pair (hi + lo, twice the MFMA work): no range limit, for inputs that
+ * the fp16 routes refuse. All compute the same function to the same bar. */
+enum { MING_ROUTE_AUTO = 0, MING_ROUTE_GENERAL = 1, MING_ROUTE_WIDE = 2 };
 
 /* Per-launch kernel timing (HIP events around each launch, on the
  * context's stream), summed per kernel family -- the reference's profile
@@ -115,6 +123,9 @@ int ming_ctx_create(int device, void* hip_stream, ming_ctx** out);
 int ming_ctx_destroy(ming_ctx* ctx);
 int ming_ctx_set_stream(ming_ctx* ctx, void* hip_stream);
 void* ming_ctx_stream(const ming_ctx* ctx);
+/* Waits for the context's stream. MING_ERR_RANGE when a projection input on
+ * an fp16 route could not be carried since the last synchronization (see
+ * MING_ROUTE_WIDE); the condition is then cleared. */
 int ming_ctx_synchronize(ming_ctx* ctx);
 int ming_ctx_engagement(const ming_ctx* ctx, ming_engagement* out);
 int ming_ctx_reset_engagement(ming_ctx* ctx);
@@ -362,7 +373,9 @@ float ming_model_lora_scale(const ming_model* m, int slot);
  * cap_embedder, the rest H-wide rows that bypass it) in device memory; the
  * joint layout's positions (host int32 [img_tokens + cap_len] per axis, image
  * rows first); out [img_tokens][patch_dim] device, the velocity before
- * negation. Synchronous: returns after the GPU finished. */
+ * negation. Synchronous: returns after the GPU finished. MING_ERR_RANGE when a
+ * projection input could not be carried in fp16 on the context's route (the
+ * output is then not valid; MING_ROUTE_WIDE runs such a forward). */
 int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* cap,
                        int64_t cap_stride, int img_tokens, int cap_len, int query_rows,
                        const int32_t* pos_t, const int32_t* pos_h, const int32_t* pos_w,

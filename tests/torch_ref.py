@@ -189,7 +189,8 @@ class Ref:
         if Q > 0:
             capn = self.rms(cap_v[:Q, :m["cap_dim"]], bf(m["cap_norm"], dev), eps)
             joint[img:img + Q] = self.r(self.lin(capn, m["cap_in"]) + bf(m["cap_in_b"], dev))
-        joint[img + Q:] = cap_v[Q:cap_len, :H]
+        if Q < cap_len:
+            joint[img + Q:] = cap_v[Q:cap_len, :H]
         for blk in m["ctx_blocks"]:
             joint[img:] = self.block(joint[img:], blk, NH, cos_t[img:], sin_t[img:], None,
                                      scales, eps)

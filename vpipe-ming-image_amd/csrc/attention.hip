@@ -315,6 +315,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
   const int q = q0 + 32 * wave + fr;
   if (q < R) {
     uint16_t* op = a.o + (long long)q * a.ldo + head * AHD + 8 * fh;
+    uint32_t seen = 0;   // magnitudes written to the fp16 copy
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -326,6 +327,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
         v.w = pack_bf16x2_rne(oacc[u][8 * hh + 6] * inv, oacc[u][8 * hh + 7] * inv);
         *reinterpret_cast<uint4*>(op + 32 * u + 16 * hh) = v;
         if (a.oh) {
+          seen = range_track4(seen, v);
           uint4 f;
           f.x = bf16x2_to_f16x2(v.x);
           f.y = bf16x2_to_f16x2(v.y);
@@ -335,6 +337,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
                                     32 * u + 16 * hh) = f;
         }
       }
+    if (a.oh) range_report(a.range, seen);
   }
 }
 

@@ -57,11 +57,36 @@ __device__ __forceinline__ float silu_f(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// Two bf16 (one u32) -> two fp16 (one u32). Exact for every value inside
-// fp16's range, so the rounding mode of the packed conversion is moot.
+// Two bf16 (one u32) -> two fp16 (one u32). Exact for every finite value of
+// magnitude below 2^16 (bf16's largest below it, 65280, is an fp16 value),
+// so the rounding mode of the packed conversion is moot there. A finite
+// value of 2^16 or more SATURATES to +-65504 (round toward zero): the
+// writers of fp16 copies track what they convert with range_track and report
+// it with range_report, and the host turns a report into MING_ERR_RANGE.
 __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u) {
   auto h = __builtin_amdgcn_cvt_pkrtz(bf16_lo(u), bf16_hi(u));
   return __builtin_bit_cast(uint32_t, h);
+}
+
+// The largest bf16 magnitude of each 16-bit half seen so far (start from 0):
+// one AND and one packed 16-bit max per converted word.
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t range_track(uint32_t seen, uint32_t w) {
+  const u16x2_t a = __builtin_bit_cast(u16x2_t, seen);
+  const u16x2_t b = __builtin_bit_cast(u16x2_t, w & 0x7fff7fffu);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+__device__ __forceinline__ uint32_t range_track4(uint32_t seen, const uint4& v) {
+  seen = range_track(seen, v.x);
+  seen = range_track(seen, v.y);
+  seen = range_track(seen, v.z);
+  return range_track(seen, v.w);
+}
+// Raises *flag (a plain store of 1; concurrent writers store the same value)
+// when a tracked magnitude is 2^16 or more, inf or NaN: a value the fp16
+// copy does not hold. Only lanes that saw one store.
+__device__ __forceinline__ void range_report(int* flag, uint32_t seen) {
+  if (flag && ((seen & 0xffffu) >= 0x4780u || (seen >> 16) >= 0x4780u)) *flag = 1;
 }
 
 // Two f32 -> two fp16, round to nearest even.

@@ -61,9 +61,15 @@ struct QprojArgs {
   // summed in slice order by a second launch (N % 4 == 0)
   float* part;
   int kslices;
+  // optional: set to 1 when an fp16 conversion of this launch (the general
+  // kernel's x tiles, the fast epilogue's yh) met a bf16 value of magnitude
+  // >= 2^16, inf or NaN (see range_report)
+  int* range;
 };
 
-hipError_t launch_qproj(int bits, const QprojArgs& a, hipStream_t s);
+// wide: bits 4/8 run with bf16 activations and the weight as a bf16 pair
+// hi + lo (two passes over K): no fp16 anywhere, any finite input.
+hipError_t launch_qproj(int bits, const QprojArgs& a, hipStream_t s, bool wide = false);
 
 // Dense attention, head dim 128: O = softmax(scale * Q K^T) V per head.
 // q, k: token-major rows (head h at column 128h); vt: V^T [NH][128][ldv]
@@ -89,6 +95,7 @@ struct AttnArgs {
   // fast projection route's input for the o-projection
   uint16_t* oh;
   long long ldoh;
+  int* range;           // optional: raised as QprojArgs::range for oh
   int R, NH;
   float sl2;
 };
@@ -129,10 +136,11 @@ hipError_t launch_rmsnorm(const uint16_t* x, long long ldx, const uint16_t* w,
                           float eps, hipStream_t s);
 // mode 0 plain; 1 also h = fp16(y); 2 h = bf16(h + tg * y) with tg = tanh(gate)
 // in f32, y unused; 3 h = bf16(h + y) (see rmsnorm_kernel)
+// `range` (optional, mode 1): raised as QprojArgs::range for the fp16 copy
 hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const uint16_t* w,
                              uint16_t* y, long long ldy, uint16_t* h, long long ldh,
                              const float* tg, int rows, int D, float eps,
-                             hipStream_t s);
+                             hipStream_t s, int* range = nullptr);
 // t[i] = tanhf(bf16 g[i]) for the two gates of a block's adaLN output:
 // g = mods + n (gate_msa) and mods + 3n (gate_mlp) -> t[0, n) and t[n, 2n)
 hipError_t launch_tanh_gates(const uint16_t* mods, int n, float* t, hipStream_t s);
@@ -167,7 +175,7 @@ hipError_t launch_norm_residual_norm(const uint16_t* sub, long long lds, const u
                                      uint16_t* h, long long ldh, const float* tg,
                                      const uint16_t* wpre, uint16_t* y, long long ldy,
                                      uint16_t* yh, long long ldyh, int rows, int D, float eps,
-                                     hipStream_t s);
+                                     hipStream_t s, int* range = nullptr);
 // The same on k alone (the attention kernel norms q itself).
 hipError_t launch_k_norm_rope(uint16_t* x, long long ld, int k_col, int rows, int n_heads,
                               const uint16_t* wk, const float* cos_t, const float* sin_t,
@@ -248,7 +256,8 @@ int dense_xa_slices(int M, int N, int K);
 hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s);
 hipError_t launch_bf16_to_f16(const uint16_t* x, long long ldx, uint16_t* y,
-                              long long ldy, int rows, int K, hipStream_t s);
+                              long long ldy, int rows, int K, hipStream_t s,
+                              int* range = nullptr);
 
 hipError_t validate_qproj_kernels();
 hipError_t validate_qproj_fast_kernels();

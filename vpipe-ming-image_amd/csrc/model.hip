@@ -727,6 +727,9 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
   prog.poll(true);
   if (hipStreamSynchronize(s) != hipSuccess)
     return rt_fail(MING_ERR_HIP, "ming_model_forward: the GPU failed");
+  // an fp16 copy that could not hold its value fails the forward (and the
+  // caption-cache entry it filled never becomes valid)
+  RC(ming::rt_take_range_fault(c, "ming_model_forward"));
   if (fill) {
     fill->valid = true;
     fill->q = Q;

@@ -39,7 +39,7 @@ template <int LPR, int CPL, int MODE>
 __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
     const uint16_t* x, long long ldx, const uint16_t* __restrict__ w,
     uint16_t* y, long long ldy, uint16_t* h, long long ldh,
-    const float* __restrict__ tg, int rows, int D, float eps) {
+    const float* __restrict__ tg, int rows, int D, float eps, int* range) {
   constexpr int RPW = 64 / LPR;  // rows per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
@@ -79,6 +79,7 @@ __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
   for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
   const float inv = 1.0f / sqrtf(ss / (float)D + eps);
   if (!live) return;
+  uint32_t seen = 0;   // magnitudes written to the fp16 copy (MODE 1)
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = sub + LPR * i;
@@ -97,6 +98,7 @@ __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
       if (MODE <= 1) {
         *reinterpret_cast<uint4*>(y + (long long)row * ldy + 8 * c) = o;
         if (MODE == 1) {
+          seen = range_track4(seen, o);
           uint4 f;
           f.x = bf16x2_to_f16x2(o.x);
           f.y = bf16x2_to_f16x2(o.y);
@@ -128,6 +130,7 @@ __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
       }
     }
   }
+  if (MODE == 1) range_report(range, seen);
 }
 
 // The post-norm + residual of MODE 2 (gated) / 3, then MODE 1 on the new
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(256, 5) void norm_residual_norm_kernel(
     const uint16_t* sub, long long lds, const uint16_t* __restrict__ wpost,
     uint16_t* h, long long ldh, const float* __restrict__ tg,
     const uint16_t* __restrict__ wpre, uint16_t* y, long long ldy, uint16_t* yh,
-    long long ldyh, int rows, int D, float eps) {
+    long long ldyh, int rows, int D, float eps, int* range) {
   constexpr int RPW = 64 / LPR;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // rows wave-uniform at LPR 64
@@ -223,6 +226,7 @@ __global__ __launch_bounds__(256, 5) void norm_residual_norm_kernel(
   for (int o = LPR / 2; o >= 1; o >>= 1) ss2 += __shfl_xor(ss2, o, 64);
   const float inv2 = 1.0f / sqrtf(ss2 / (float)D + eps);
   if (!live) return;
+  uint32_t seen = 0;   // magnitudes written to the fp16 copy
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = sb + LPR * i;
@@ -239,6 +243,7 @@ __global__ __launch_bounds__(256, 5) void norm_residual_norm_kernel(
         ou[e] = pack_bf16x2_rne(a, b);
       }
       *reinterpret_cast<uint4*>(y + rr * ldy + 8 * c) = o;
+      seen = range_track4(seen, o);
       uint4 f;
       f.x = bf16x2_to_f16x2(o.x);
       f.y = bf16x2_to_f16x2(o.y);
@@ -247,6 +252,7 @@ __global__ __launch_bounds__(256, 5) void norm_residual_norm_kernel(
       *reinterpret_cast<uint4*>(yh + rr * ldyh + 8 * c) = f;
     }
   }
+  range_report(range, seen);
 }
 
 // cos/sin [n][head_dim/2] from three integer positions per row: pairs
@@ -319,13 +325,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const uint16_t* w,
                              uint16_t* y, long long ldy, uint16_t* h, long long ldh,
                              const float* tg, int rows, int D, float eps,
-                             hipStream_t s) {
+                             hipStream_t s, int* range) {
   if (rows <= 0) return hipSuccess;
   const int nch = D / 8;
   if (D % 8 != 0 || nch > 64 * 16 || mode < 0 || mode > 3) return hipErrorInvalidValue;
 #define MING_RMS_M(LPR, CPL, MODE)                                                \
   hipLaunchKernelGGL((rmsnorm_kernel<LPR, CPL, MODE>), dim3((rows + rpb - 1) / rpb), \
-                     dim3(256), 0, s, x, ldx, w, y, ldy, h, ldh, tg, rows, D, eps)
+                     dim3(256), 0, s, x, ldx, w, y, ldy, h, ldh, tg, rows, D, eps, range)
 #define MING_RMS(LPR, CPL)                                                     \
   do {                                                                         \
     const int rpb = 4 * (64 / (LPR));                                          \
@@ -350,14 +356,14 @@ hipError_t launch_norm_residual_norm(const uint16_t* sub, long long lds, const u
                                      uint16_t* h, long long ldh, const float* tg,
                                      const uint16_t* wpre, uint16_t* y, long long ldy,
                                      uint16_t* yh, long long ldyh, int rows, int D, float eps,
-                                     hipStream_t s) {
+                                     hipStream_t s, int* range) {
   if (rows <= 0) return hipSuccess;
   const int nch = D / 8;
   if (D % 8 != 0 || nch > 64 * 16) return hipErrorInvalidValue;
 #define MING_NRN_G(LPR, CPL, G)                                                          \
   hipLaunchKernelGGL((norm_residual_norm_kernel<LPR, CPL, G>), dim3((rows + rpb - 1) / rpb), \
                      dim3(256), 0, s, sub, lds, wpost, h, ldh, tg, wpre, y, ldy, yh, ldyh,   \
-                     rows, D, eps)
+                     rows, D, eps, range)
 #define MING_NRN(LPR, CPL)                                                     \
   do {                                                                         \
     const int rpb = 4 * (64 / (LPR));                                          \

@@ -86,6 +86,37 @@ __device__ __forceinline__ uint4 dequant8_w8(uint32_t w0, uint32_t w1,
   return o;
 }
 
+// The wide route's weights: w = fma(code, s, b) in f32 as a pair of bf16
+// hi = bf16(w), lo = bf16(w - hi) (the difference is exact in f32), so
+// hi + lo carries w to ~2^-17 relative; `lo` picks the member a tile holds.
+__device__ __forceinline__ uint32_t wide_pair(float v0, float v1, bool lo) {
+  const uint32_t hi = pack_bf16x2_rne(v0, v1);
+  if (!lo) return hi;
+  return pack_bf16x2_rne(v0 - bf16_lo(hi), v1 - bf16_hi(hi));
+}
+
+__device__ __forceinline__ uint4 dequant8_w4_wide(uint32_t w, float s, float b, bool lo) {
+  uint4 o;
+  uint32_t* op = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float c0 = (float)((w >> (4 * p)) & 15u);
+    const float c1 = (float)((w >> (4 * p + 16)) & 15u);
+    op[p] = wide_pair(fmaf(c0, s, b), fmaf(c1, s, b), lo);
+  }
+  return o;
+}
+
+__device__ __forceinline__ uint4 dequant8_w8_wide(uint32_t w0, uint32_t w1, float s, float b,
+                                                  bool lo) {
+  uint4 o;
+  o.x = wide_pair(fmaf((float)(w0 & 255u), s, b), fmaf((float)((w0 >> 8) & 255u), s, b), lo);
+  o.y = wide_pair(fmaf((float)((w0 >> 16) & 255u), s, b), fmaf((float)(w0 >> 24), s, b), lo);
+  o.z = wide_pair(fmaf((float)(w1 & 255u), s, b), fmaf((float)((w1 >> 8) & 255u), s, b), lo);
+  o.w = wide_pair(fmaf((float)((w1 >> 16) & 255u), s, b), fmaf((float)(w1 >> 24), s, b), lo);
+  return o;
+}
+
 __device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 v) {
   uint4 o;
   o.x = bf16x2_to_f16x2(v.x);
@@ -95,8 +126,12 @@ __device__ __forceinline__ uint4 bf16x8_to_f16x8(uint4 v) {
   return o;
 }
 
-template <int BITS>
+// WIDE (bits 4/8): x stays bf16 and each weight tile is the hi or the lo
+// member of its bf16 pair; K is walked twice (hi, then lo) into the same
+// accumulators on bf16 MFMA, so no value passes through fp16.
+template <int BITS, bool WIDE>
 __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
+  constexpr bool F16 = BITS != 16 && !WIDE;   // fp16 x tiles and weights
   __shared__ uint4 lds[2][2][BM * CH];  // [buf][0: x, 1: w][row*8+chunk]
 
   const int tid = threadIdx.x;
@@ -138,6 +173,7 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
   uint4 xr[8];
   uint4 wr[8];
   uint32_t sbr = 0;
+  uint32_t seen = 0;   // magnitudes converted to fp16 (range_report)
 
   const int fr = lane & 31, fk = lane >> 5;
   floatx16_t acc[4][4];
@@ -173,7 +209,7 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
       sbr = a.sb[(long long)kt * a.N + wrow];
     }
   };
-  auto store_base = [&](int buf) {
+  auto store_base = [&](int buf, bool lo) {
     uint4* lx = lds[buf][0];
     uint4* lw = lds[buf][1];
     if constexpr (BITS == 16) {
@@ -184,17 +220,28 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) lx[swz(pr + 32 * i, pc)] = bf16x8_to_f16x8(xr[i]);
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (F16) {
+          seen = range_track4(seen, xr[i]);
+          lx[swz(pr + 32 * i, pc)] = bf16x8_to_f16x8(xr[i]);
+        } else {
+          lx[swz(pr + 32 * i, pc)] = xr[i];
+        }
+      }
       const float s = bf16_lo(sbr), b = bf16_hi(sbr);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         uint4 d;
         if constexpr (BITS == 4) {
           const uint32_t w = j < 4 ? (&wr[0].x)[j] : (&wr[1].x)[j - 4];
-          d = dequant8_w4(w, s, b);
+          d = F16 ? dequant8_w4(w, s, b) : dequant8_w4_wide(w, s, b, lo);
         } else {
           const uint4 q = wr[j >> 1];
-          d = (j & 1) ? dequant8_w8(q.z, q.w, s, b) : dequant8_w8(q.x, q.y, s, b);
+          if constexpr (F16)
+            d = (j & 1) ? dequant8_w8(q.z, q.w, s, b) : dequant8_w8(q.x, q.y, s, b);
+          else
+            d = (j & 1) ? dequant8_w8_wide(q.z, q.w, s, b, lo)
+                        : dequant8_w8_wide(q.x, q.y, s, b, lo);
         }
         lw[swz(tid, j)] = d;
       }
@@ -272,26 +319,30 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
     }
   };
 
-  // Base K loop: one barrier per stage; stage kt+1 is fetched into
-  // registers before stage kt's MFMAs and stored to the other buffer
-  // after them.
+  // Base K loop: one barrier per stage; stage s+1 is fetched into
+  // registers before stage s's MFMAs and stored to the other buffer after
+  // them. The wide route's stages KT..2KT-1 walk K again with the lo weights.
+  constexpr int PASSES = (WIDE && BITS != 16) ? 2 : 1;
+  const int KS = KT * PASSES;
   load_base(0);
-  store_base(0);
+  store_base(0, false);
   __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) load_base(kt + 1);
+  for (int st = 0; st < KS; ++st) {
+    const int cur = st & 1;
+    const bool more = st + 1 < KS;
+    const bool next_lo = st + 1 >= KT;
+    if (more) load_base(next_lo ? st + 1 - KT : st + 1);
     else if (chunks > 0) load_tail(0);
-    if constexpr (BITS == 16) compute_bf16(cur);
-    else compute_f16(cur);
-    if (more) store_base(cur ^ 1);
+    if constexpr (F16) compute_f16(cur);
+    else compute_bf16(cur);
+    if (more) store_base(cur ^ 1, next_lo);
     else if (chunks > 0) store_tail(cur ^ 1);
     __syncthreads();
   }
+  if constexpr (F16) range_report(a.range, seen);
   // LoRA tail: the live ranks, appended along K.
   for (int ch = 0; ch < chunks; ++ch) {
-    const int cur = (KT + ch) & 1;
+    const int cur = (KS + ch) & 1;
     const bool more = ch + 1 < chunks;
     if (more) load_tail(ch + 1);
     compute_bf16(cur);
@@ -448,13 +499,20 @@ __global__ void repack_sb_kernel(const uint16_t* scales, const uint16_t* biases,
 
 }  // namespace
 
-hipError_t launch_qproj(int bits, const QprojArgs& a, hipStream_t s) {
+hipError_t launch_qproj(int bits, const QprojArgs& a, hipStream_t s, bool wide) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return hipSuccess;
+  const dim3 g(tiles), b(NT);
   switch (bits) {
-    case 4: hipLaunchKernelGGL(qproj_kernel<4>, dim3(tiles), dim3(NT), 0, s, a); break;
-    case 8: hipLaunchKernelGGL(qproj_kernel<8>, dim3(tiles), dim3(NT), 0, s, a); break;
-    case 16: hipLaunchKernelGGL(qproj_kernel<16>, dim3(tiles), dim3(NT), 0, s, a); break;
+    case 4:
+      if (wide) hipLaunchKernelGGL((qproj_kernel<4, true>), g, b, 0, s, a);
+      else hipLaunchKernelGGL((qproj_kernel<4, false>), g, b, 0, s, a);
+      break;
+    case 8:
+      if (wide) hipLaunchKernelGGL((qproj_kernel<8, true>), g, b, 0, s, a);
+      else hipLaunchKernelGGL((qproj_kernel<8, false>), g, b, 0, s, a);
+      break;
+    case 16: hipLaunchKernelGGL((qproj_kernel<16, false>), g, b, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -487,9 +545,11 @@ namespace ming {
 hipError_t validate_qproj_kernels() {
   hipFuncAttributes fa;
   const void* fns[] = {
-      reinterpret_cast<const void*>(&qproj_kernel<4>),
-      reinterpret_cast<const void*>(&qproj_kernel<8>),
-      reinterpret_cast<const void*>(&qproj_kernel<16>),
+      reinterpret_cast<const void*>(&qproj_kernel<4, false>),
+      reinterpret_cast<const void*>(&qproj_kernel<8, false>),
+      reinterpret_cast<const void*>(&qproj_kernel<16, false>),
+      reinterpret_cast<const void*>(&qproj_kernel<4, true>),
+      reinterpret_cast<const void*>(&qproj_kernel<8, true>),
       reinterpret_cast<const void*>(&lora_xa_kernel),
       reinterpret_cast<const void*>(&repack_codes_kernel),
       reinterpret_cast<const void*>(&repack_sb_kernel)};

@@ -534,6 +534,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
   const bool st16 = (a.ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
   const int cl = lane & 7;
   const int n = n0 + 64 * wave + 8 * cl;
+  uint32_t seen = 0;   // magnitudes written to the fp16 copy (range_report)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     // Fused SwiGLU: this half's gate rows are loaded first, so their memory
@@ -587,6 +588,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
           reinterpret_cast<uint2*>(yp)[1] = make_uint2(v.z, v.w);
         }
         if (a.yh) {
+          seen = range_track4(seen, v);
           uint4 f;
           f.x = bf16x2_to_f16x2(v.x);
           f.y = bf16x2_to_f16x2(v.y);
@@ -597,6 +599,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
       }
     }
   }
+  if (a.yh) range_report(a.range, seen);
 }
 
 // The split projection's end: y = bf16(sum of the slices in order), then as
@@ -604,6 +607,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 __global__ void qproj_split_reduce_kernel(const QprojArgs a) {
   const int n4 = a.N >> 2;
   const long long total = (long long)a.M * n4;
+  uint32_t seen = 0;
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
        i += (long long)gridDim.x * blockDim.x) {
     const long long m = i / n4;
@@ -623,10 +627,13 @@ __global__ void qproj_split_reduce_kernel(const QprojArgs a) {
                                 silu_f(bf16_hi(gp[e])) * bf16_hi(vp[e]));
     }
     *reinterpret_cast<uint2*>(a.y + m * a.ldy + n) = make_uint2(vp[0], vp[1]);
-    if (a.yh)
+    if (a.yh) {
+      seen = range_track(range_track(seen, vp[0]), vp[1]);
       *reinterpret_cast<uint2*>(a.yh + m * a.ldyh + n) =
           make_uint2(bf16x2_to_f16x2(vp[0]), bf16x2_to_f16x2(vp[1]));
+    }
   }
+  range_report(a.range, seen);
 }
 
 // ---- T = x . A_live^T * coef: the adapters' stacked down-projection --------
@@ -906,14 +913,16 @@ __global__ void repack_sbf_kernel(const uint16_t* scales, const uint16_t* biases
 }
 
 __global__ void bf16_to_f16_kernel(const uint16_t* x, long long ldx, uint16_t* y,
-                                   long long ldy, int rows, int K) {
+                                   long long ldy, int rows, int K, int* range) {
   const int k8 = K >> 3;
   const long long total = (long long)rows * k8;
+  uint32_t seen = 0;
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
        i += (long long)gridDim.x * blockDim.x) {
     const long long r = i / k8;
     const int c = (int)(i % k8) * 8;
     const uint4 v = *reinterpret_cast<const uint4*>(x + r * ldx + c);
+    seen = range_track4(seen, v);
     uint4 o;
     o.x = bf16x2_to_f16x2(v.x);
     o.y = bf16x2_to_f16x2(v.y);
@@ -921,6 +930,7 @@ __global__ void bf16_to_f16_kernel(const uint16_t* x, long long ldx, uint16_t* y
     o.w = bf16x2_to_f16x2(v.w);
     *reinterpret_cast<uint4*>(y + r * ldy + c) = o;
   }
+  range_report(range, seen);
 }
 
 }  // namespace
@@ -1015,13 +1025,13 @@ hipError_t launch_repack_fast(int bits, const uint32_t* codes,
 }
 
 hipError_t launch_bf16_to_f16(const uint16_t* x, long long ldx, uint16_t* y,
-                              long long ldy, int rows, int K, hipStream_t s) {
+                              long long ldy, int rows, int K, hipStream_t s, int* range) {
   long long work = (long long)rows * (K / 8);
   long long blocks = (work + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(bf16_to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     s, x, ldx, y, ldy, rows, K);
+                     s, x, ldx, y, ldy, rows, K, range);
   return hipGetLastError();
 }
 

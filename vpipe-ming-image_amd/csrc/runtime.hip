@@ -80,6 +80,9 @@ struct ming_ctx {
   void* part = nullptr;        // split-K partials of the stacked x.A GEMM
   size_t part_bytes = 0;
   int route = MING_ROUTE_AUTO;
+  // device word raised by any fp16 copy that could not hold its value
+  // (range_report); read and cleared at synchronization points
+  int* range = nullptr;
   int live_weights = 0;   // a context outlives every weight made on it
   // Per-launch HIP-event timing (ming_ctx_set_profiling), by bucket.
   bool profiling = false;
@@ -355,6 +358,32 @@ void destroy_qweight(ming_qweight* q) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// The range word the kernels raise: on the fp16 routes (auto, general);
+// the wide route converts nothing to fp16, and whatever fp16 copies the block
+// driver still writes there are not read.
+int* range_word(const ming_ctx* c) {
+  return c->route == MING_ROUTE_WIDE ? nullptr : c->range;
+}
+
+// Reads the range word after the stream has drained: raised means some
+// projection input on an fp16 route was >= 2^16 in magnitude or not finite,
+// and its fp16 copy did not hold it. Cleared, counted and reported.
+int take_range_fault(ming_ctx* c, const char* who) {
+  int h = 0;
+  MING_HIP(hipMemcpyAsync(&h, c->range, sizeof(int), hipMemcpyDeviceToHost, c->stream),
+           "range word read");
+  MING_HIP(hipStreamSynchronize(c->stream), "range word read");
+  if (h == 0) return MING_OK;
+  MING_HIP(hipMemsetAsync(c->range, 0, sizeof(int), c->stream), "range word reset");
+  c->eng.range_faults += 1;
+  return fail(MING_ERR_RANGE,
+              std::string(who) +
+                  ": a projection input on an fp16 route had a value of magnitude >= 65536 "
+                  "or not finite, which its fp16 copy cannot hold; the results since the "
+                  "last synchronization are not valid (MING_ROUTE_WIDE computes such inputs "
+                  "in bf16)");
+}
+
 }  // namespace
 
 extern "C" {
@@ -400,6 +429,14 @@ int ming_ctx_create(int device, void* hip_stream, ming_ctx** out) {
     }
     c->own_stream = true;
   }
+  if (hipMalloc(&c->range, 256) != hipSuccess ||
+      hipMemsetAsync(c->range, 0, sizeof(int), c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess) {
+    if (c->range) (void)hipFree(c->range);
+    if (c->own_stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return fail(MING_ERR_HIP, "ming_ctx_create: range word allocation failed");
+  }
   *out = c;
   return ok();
 }
@@ -417,6 +454,7 @@ int ming_ctx_destroy(ming_ctx* c) {
   if (c->vt) (void)hipFree(c->vt);
   if (c->up) (void)hipFree(c->up);
   if (c->part) (void)hipFree(c->part);
+  if (c->range) (void)hipFree(c->range);
   for (auto& rec : c->recs) {
     (void)hipEventDestroy(rec.a);
     (void)hipEventDestroy(rec.b);
@@ -443,6 +481,8 @@ int ming_ctx_synchronize(ming_ctx* c) {
   if (!c) return fail(MING_ERR_ARG, "null context");
   DeviceGuard g(c->device);
   MING_HIP(hipStreamSynchronize(c->stream), "synchronize");
+  const int rc = take_range_fault(c, "ming_ctx_synchronize");
+  if (rc != MING_OK) return rc;
   return ok();
 }
 
@@ -778,7 +818,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
   // A handful of rows and no live adapter (the adaLN and timestep
   // projections run at M = 1): the GEMV streams each weight once instead of
   // running a 256-row tile.
-  if (c->route == MING_ROUTE_AUTO && M <= ming::kGemvMaxM) {
+  if (c->route != MING_ROUTE_GENERAL && M <= ming::kGemvMaxM) {
     bool gemv = true;
     for (int i = 0; i < n && gemv; ++i) {
       const ming_qweight* q = qs[i];
@@ -930,7 +970,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       if (qa[i].seg[si].chunks > 0 &&
           (uint64_t)q->segs[si].N * (uint64_t)q->b_ld[si] * 2 > (1ull << 32))
         fits32 = false;
-    fast[i] = q->bits != 16 && q->fast && c->route != MING_ROUTE_GENERAL && fits32;
+    fast[i] = q->bits != 16 && q->fast && c->route == MING_ROUTE_AUTO && fits32;
     any_fast = any_fast || fast[i];
   }
   // The fast route reads x as fp16 carrying the same (bf16) values: one
@@ -942,7 +982,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     uint16_t* dst = (uint16_t*)c->xh;
     MING_HIP(profiled(c, kBCvt, 0.0, 4.0 * M * K,
                       [&] { return ming::launch_bf16_to_f16(x, ldx, dst, K, M, K,
-                                                            c->stream); }),
+                                                            c->stream, range_word(c)); }),
              "bf16->fp16 launch");
     xh = dst;
   }
@@ -955,6 +995,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     a.t = T; a.ldt = t_cols > 0 ? t_cols : 0; a.nseg = (int)q->segs.size();
     a.g = nullptr; a.ldg = 0;
     a.yh = nullptr; a.ldyh = 0;
+    a.range = range_word(c);
     if (o.gate && !fast[i]) {
       // the general route writes the projection first: into a plane of its
       // own, since y may be the gate itself
@@ -991,7 +1032,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     // columns: 16) runs as the x.A path's split-K bf16 GEMM -- identity
     // column groups, coefficient 1 -- which spreads K over the chip.
     const bool dense_sk =
-        q->bits == 16 && c->route == MING_ROUTE_AUTO && live_segs[i] == 0 && !o.gate &&
+        q->bits == 16 && c->route != MING_ROUTE_GENERAL && live_segs[i] == 0 && !o.gate &&
         !o.yh && ((M + 255) / 256) * ((q->N + 255) / 256) < 64 && q->N % 64 == 0 &&
         q->N <= 16 * ming::kMaxGroups && K % 64 == 0 && o.ldy <= (1 << 30) &&
         (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) &&
@@ -1018,7 +1059,8 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
                         2.0 * M * K + wbytes + 2.0 * M * q->N,
                         [&] {
                           return fast[i] ? ming::launch_qproj_fast(q->bits, a, c->stream)
-                                         : ming::launch_qproj(q->bits, a, c->stream);
+                                         : ming::launch_qproj(q->bits, a, c->stream,
+                                                              c->route == MING_ROUTE_WIDE);
                         }),
                "qproj launch");
     }
@@ -1137,7 +1179,8 @@ static int rms_impl(ming_ctx* c, int mode, const uint16_t* x, int64_t ldx,
   const double bytes = (mode == 0 ? 4.0 : 6.0) * rows * D + (mode == 2 ? 6.0 : 2.0) * D;
   MING_HIP(profiled(c, mode >= 2 ? kBNormRes : kBRms, 0.0, bytes,
                     [&] { return ming::launch_rmsnorm_ex(mode, x, ldx, w, y, ldy, h, ldh,
-                                                         gate, rows, D, eps, c->stream); }),
+                                                         gate, rows, D, eps, c->stream,
+                                                         range_word(c)); }),
            "rmsnorm launch");
   c->eng.rmsnorm += 1;
   if (mode >= 2) c->eng.elementwise += 1;
@@ -1241,6 +1284,7 @@ static int attention_impl(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_co
     if (rc != MING_OK) return rc;
     a.oh = (uint16_t*)c->xh;
     a.ldoh = w;
+    a.range = range_word(c);
   }
   a.R = rows; a.NH = n_heads;
   a.sl2 = scale * 1.4426950408889634f;
@@ -1275,7 +1319,7 @@ int ming_attention(ming_ctx* c, const uint16_t* qkv, int64_t ld, int q_col, int 
 
 int ming_ctx_set_route(ming_ctx* c, int route) {
   if (!c) return fail(MING_ERR_ARG, "null context");
-  if (route != MING_ROUTE_AUTO && route != MING_ROUTE_GENERAL)
+  if (route != MING_ROUTE_AUTO && route != MING_ROUTE_GENERAL && route != MING_ROUTE_WIDE)
     return fail(MING_ERR_ARG, "ming_ctx_set_route: unknown route");
   c->route = route;
   return ok();
@@ -1537,6 +1581,11 @@ void rt_free(ming_ctx* c, void* dev) {
 
 void rt_note_cap_hit(ming_ctx* c) { c->eng.cap_cache_hits += 1; }
 
+int rt_take_range_fault(ming_ctx* c, const char* who) {
+  DeviceGuard dg(c->device);
+  return take_range_fault(c, who);
+}
+
 int rt_rmsnorm_f16(ming_ctx* c, const uint16_t* x, int64_t ldx, const uint16_t* w,
                    uint16_t* y, int64_t ldy, int rows, int D, float eps) {
   return rms_impl(c, 1, x, ldx, w, y, ldy, nullptr, 0, nullptr, rows, D, eps, "rmsnorm");
@@ -1569,7 +1618,8 @@ int rt_norm_residual_norm(ming_ctx* c, uint16_t* h, int64_t ldh, const uint16_t*
   MING_HIP(profiled(c, kBNormRes, 0.0, 10.0 * rows * D + (tgate ? 8.0 : 4.0) * D,
                     [&] { return ming::launch_norm_residual_norm(sub, lds, wpost, h, ldh, tgate,
                                                                  wpre, y, ldy, yh, D, rows, D,
-                                                                 eps, c->stream); }),
+                                                                 eps, c->stream,
+                                                                 range_word(c)); }),
            "norm-residual-norm launch");
   // counted as the two launches it replaces
   c->eng.rmsnorm += 2;
@@ -1596,7 +1646,7 @@ int rt_modulation_batch(ming_ctx* c, int count, const ming_qweight* const* ada,
                         uint16_t* const* mods, uint16_t* const* nw1, uint16_t* const* nw3,
                         float* const* tg, const float* scales, bool* done) {
   *done = false;
-  if (count <= 0 || c->route != MING_ROUTE_AUTO || !ada[0]) return ok();
+  if (count <= 0 || c->route == MING_ROUTE_GENERAL || !ada[0]) return ok();
   const ming_qweight* q0 = ada[0];
   for (int i = 0; i < count; ++i) {
     const ming_qweight* q = ada[i];

@@ -51,16 +51,20 @@ def close_all():
                     pass
 
 
-def _finalize(obj):
+def _finalize(obj, _finalizing=sys.is_finalizing):
     """__del__ body: close, unless the interpreter is shutting down (then the
     atexit hook has closed what was open, and a late call into the HIP
-    runtime could run after its teardown)."""
-    if sys.is_finalizing():
+    runtime could run after its teardown). What it calls is bound at
+    definition: module globals read None during interpreter teardown."""
+    if _finalizing():
         return
     try:
         obj.close()
     except Exception:
         pass
+
+
+ERR_RANGE = 7
 
 
 class MingError(RuntimeError):
@@ -311,8 +315,8 @@ class Ctx:
             _check(lib().ming_ctx_destroy(self.h))
             self.h = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
     def set_stream(self, stream: int | None):
         _check(lib().ming_ctx_set_stream(self.h, stream))
@@ -329,8 +333,10 @@ class Ctx:
         _check(lib().ming_ctx_reset_engagement(self.h))
 
     def set_route(self, route: str = "auto"):
-        """'auto' (fast route when the weight allows it) or 'general'."""
-        _check(lib().ming_ctx_set_route(self.h, {"auto": 0, "general": 1}[route]))
+        """'auto' (fast route when the weight allows it), 'general' (the general
+        kernel) or 'wide' (bf16 activations and bf16-pair weights: no fp16
+        range limit)."""
+        _check(lib().ming_ctx_set_route(self.h, {"auto": 0, "general": 1, "wide": 2}[route]))
 
     def set_profiling(self, on: bool = True):
         _check(lib().ming_ctx_set_profiling(self.h, int(on)))
@@ -520,8 +526,8 @@ class QWeight:
             lib().ming_qweight_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 def _h(obj) -> int | None:
@@ -627,8 +633,8 @@ class Pack:
             lib().ming_pack_close(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 def pack_write(src_dir: str, dst_dir: str, bits: int, threads: int = 0):
@@ -763,8 +769,8 @@ class Model:
             lib().ming_model_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 def header_symbols(path: str = HEADER):
