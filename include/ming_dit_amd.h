@@ -191,6 +191,27 @@ int ming_lin(ming_ctx* ctx, const ming_qweight* qw, const uint16_t* x,
              int64_t ldx, uint16_t* y, int64_t ldy, int M,
              const float* scales);
 
+/* ming_lin that allocates nothing. It has NO counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and bits as ming_lin; the call's scratch (the adapters'
+ * x.A intermediate, the fp16 copy of x, split-K partials) comes from one
+ * static array of MING_NOALLOC_SCRATCH_BYTES per GPU, resident from the first
+ * context on that GPU until the process ends. Refusals, before anything is
+ * launched: MING_ERR_SHAPE when a call needs more than the array holds (the
+ * fp16 copy of x, M * K * 2 bytes; the adapters' x.A intermediate, M * padded
+ * live ranks * 2 bytes; the f32 partials of a split-K launch, slices * M *
+ * columns * 4 bytes; each region rounded up to 256 bytes); MING_ERR_STATE
+ * when the weight's adapter bindings changed since its last ming_lin call
+ * (that call builds the stacked factors, which allocates). Every call on a
+ * GPU shares that GPU's array and it keeps the last call's contents (nothing
+ * in it needs to start at zero): calls that overlap on one GPU -- other
+ * streams, other contexts, other threads -- race. Profiling events are not
+ * recorded for it. */
+#define MING_NOALLOC_SCRATCH_BYTES (64u << 20)
+int ming_lin_noalloc(ming_ctx* ctx, const ming_qweight* w, const uint16_t* x,
+                     int64_t ldx, uint16_t* y, int64_t ldy, int M, const float* scales);
+
 /* out = bf16(silu(g) * bf16(lin(x, w))): the w3 projection with the SwiGLU
  * of gpu_ff (ming-dit.cc:2151-2158; ming_ops.metal:97-112) fused into its
  * epilogue. Same bits as ming_lin then ming_swiglu. g may be out (in place).

@@ -86,6 +86,7 @@ struct ming_ctx {
   int live_weights = 0;   // a context outlives every weight made on it
   // Per-launch HIP-event timing (ming_ctx_set_profiling), by bucket.
   bool profiling = false;
+  bool no_events = false;   // set while ming_lin_noalloc runs (creating one may allocate)
   struct Rec { int bucket; hipEvent_t a, b; double flops, bytes; };
   std::vector<Rec> recs;
   std::vector<hipEvent_t> pool;
@@ -120,7 +121,7 @@ hipEvent_t take_event(ming_ctx* c) {
 template <class F>
 hipError_t profiled(ming_ctx* c, int bucket, double flops, double bytes,
                     F&& launch) {
-  if (!c->profiling) return launch();
+  if (!c->profiling || c->no_events) return launch();
   hipEvent_t a = take_event(c), b = take_event(c);
   if (!a || !b) return hipErrorOutOfMemory;
   hipError_t e = hipEventRecord(a, c->stream);
@@ -358,6 +359,37 @@ void destroy_qweight(ming_qweight* q) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// ---- scratch of the entry point that allocates nothing (ming_lin_noalloc) --
+// One array per GPU, resident for the life of the process. Host code never
+// uses its name as an address (in host code it is only a stand-in symbol):
+// each device's address is taken with hipGetSymbolAddress when the first
+// context on that device is created, with the device current.
+static __device__ __align__(256) unsigned char scratch[MING_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up once (device current).
+int noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(MING_ERR_ARG, "no-alloc scratch: device index out of range");
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (g_noalloc_ptr[device]) return MING_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return fail(MING_ERR_HIP, std::string("no-alloc scratch: hipGetSymbolAddress failed: ") +
+                                  hipGetErrorString(e));
+  g_noalloc_ptr[device] = p;
+  return MING_OK;
+}
+
+void* noalloc_ptr(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  return g_noalloc_ptr[device];
+}
+
 // The range word the kernels raise: on the fp16 routes (auto, general);
 // the wide route converts nothing to fp16, and whatever fp16 copies the block
 // driver still writes there are not read.
@@ -417,6 +449,11 @@ int ming_ctx_create(int device, void* hip_stream, ming_ctx** out) {
                 std::string("kernel validation failed on this device (the "
                             "library is built for gfx950): ") +
                     hipGetErrorString(e));
+  // the device's no-alloc scratch address (its array is resident already)
+  {
+    const int rc = noalloc_setup(device);
+    if (rc != MING_OK) return rc;
+  }
   auto* c = new (std::nothrow) ming_ctx();
   if (!c) return fail(MING_ERR_ALLOC, "ming_ctx_create: out of memory");
   c->device = device;
@@ -785,9 +822,24 @@ struct LinOut {
 // stacked x.A launch -- the stacks' 16-rank groups side by side in T, group
 // entries naming their weight -- before each projection's GEMM reads its own
 // columns of T. n == 1 is lin() (ming-dit.cc:1763-1771).
+// Where one call's scratch comes from: the context's buffers, grown on
+// demand (every entry point but one), or regions carved from the device's
+// static no-alloc array (ming_lin_noalloc), sized before anything launches.
+struct Carve {
+  char* base = nullptr;
+  size_t cap = 0, used = 0;
+  static size_t aligned256(size_t b) { return (b + 255) & ~(size_t)255; }
+  // a 256-byte-aligned region of `bytes` (callers check the total first)
+  void* take(size_t bytes) {
+    void* p = base + used;
+    used += aligned256(bytes);
+    return p;
+  }
+};
+
 static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const LinOut* outs,
                      const uint16_t* x, int64_t ldx, int M, const float* scales,
-                     const uint16_t* xh_src) {
+                     const uint16_t* xh_src, Carve* carve = nullptr) {
   for (int i = 0; i < n; ++i)
     if (outs[i].took_fast) *outs[i].took_fast = false;
   if (!c || !x || n < 1 || n > ming::kMaxXaSources)
@@ -817,7 +869,8 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
 
   // A handful of rows and no live adapter (the adaLN and timestep
   // projections run at M = 1): the GEMV streams each weight once instead of
-  // running a 256-row tile.
+  // running a 256-row tile. It reads bf16 x in f32, so any route but the
+  // general one takes it.
   if (c->route != MING_ROUTE_GENERAL && M <= ming::kGemvMaxM) {
     bool gemv = true;
     for (int i = 0; i < n && gemv; ++i) {
@@ -849,6 +902,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     }
   }
 
+  // ---- plan: the live stacks, the routes, and every scratch size --------
   // The live stacks, per weight and segment, in slot order.
   ming::QprojArgs qa[ming::kMaxXaSources] = {};
   ming::LoraXaArgs xa{};
@@ -865,6 +919,10 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       for (int sl = 0; sl < MING_MAX_LORA_SLOTS; ++sl)
         if (q->segs[si].slot[sl].rank > 0 && scales && scales[sl] != 0.0f) any_live = true;
     if (any_live) {
+      if (carve && q->stacks_dirty)
+        return fail(MING_ERR_STATE,
+                    "ming_lin_noalloc: the weight's adapter stacks are not built since its "
+                    "last binding change (one ming_lin call builds them)");
       int rc = build_stacks(q);
       if (rc != MING_OK) return rc;
       xa.A[i] = q->A_all;
@@ -926,37 +984,12 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     ++xa_groups;
   }
   const int t_cols = xa_groups * 16;
-  uint16_t* T = nullptr;
-  if (t_cols > 0) {
-    int rc = ensure_scratch(c, (size_t)M * t_cols * 2);
-    if (rc != MING_OK) return rc;
-    T = (uint16_t*)c->scratch;
-    xa.x = x; xa.ldx = ldx; xa.K = K; xa.M = M;
-    xa.n_cols = t_cols; xa.t = T; xa.ldt = t_cols;
-    // the fast x.A addresses x and each A stack as 64-bit bases plus 32-bit
-    // byte offsets
-    const bool xa_fast = c->route != MING_ROUTE_GENERAL && ldx % 8 == 0 &&
-                         (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) && xa_fits;
-    int ks = 1;
-    if (xa_fast) {
-      ks = ming::lora_xa_fast_slices(M, t_cols, K);
-      if (ks > 1) {
-        rc = ensure_part(c, (size_t)ks * M * t_cols * 4);
-        if (rc != MING_OK) return rc;
-      }
-    }
-    double a_bytes = 0.0;
-    for (int i = 0; i < n; ++i)
-      if (xa.A[i]) a_bytes += 2.0 * qs[i]->a_rows * (double)K;
-    MING_HIP(profiled(c, kBXa, xa_flops, 2.0 * M * K + a_bytes + 2.0 * M * t_cols,
-                      [&] {
-                        return xa_fast ? ming::launch_lora_xa_fast(xa, (float*)c->part,
-                                                                   ks, c->stream)
-                                       : ming::launch_lora_xa(xa, c->stream);
-                      }),
-             "lora_xa launch");
-    c->eng.lora_xa += 1;
-  }
+  // the fast x.A addresses x and each A stack as 64-bit bases plus 32-bit
+  // byte offsets; its K split (slices summed in f32 by a second launch)
+  const bool xa_fast = t_cols > 0 && c->route != MING_ROUTE_GENERAL && ldx % 8 == 0 &&
+                       (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) && xa_fits;
+  const int xa_ks = xa_fast ? ming::lora_xa_fast_slices(M, t_cols, K) : 1;
+  size_t part_bytes = xa_ks > 1 ? (size_t)xa_ks * M * t_cols * 4 : 0;
   // Which projections take the fast route. It addresses each operand as a
   // 64-bit base plus 32-bit byte offsets: x (fp16 copy, row stride K), T and
   // every B stack must fit.
@@ -973,18 +1006,96 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     fast[i] = q->bits != 16 && q->fast && c->route == MING_ROUTE_AUTO && fits32;
     any_fast = any_fast || fast[i];
   }
+  // Per projection: the fast route's K split on few tiles (the context
+  // refiner's 256 caption rows: 15 or 40 tiles), about one round of the
+  // chip at >= 6 K steps a slice; a dense weight with no live adapter on few
+  // 256 x 256 tiles (the caption embedder: 15; the final layer's 64
+  // columns: 16) runs as the x.A path's split-K bf16 GEMM (identity column
+  // groups, coefficient 1); the general route writes a gated projection into
+  // a plane of its own first, since y may be the gate itself.
+  int split_ks[ming::kMaxXaSources] = {};
+  int dense_ks[ming::kMaxXaSources] = {};
+  size_t up_bytes = 0;
+  for (int i = 0; i < n; ++i) {
+    const ming_qweight* q = qs[i];
+    const LinOut& o = outs[i];
+    const int tiles = ((M + 255) / 256) * ((q->N + 255) / 256);
+    if (fast[i] && tiles < 64 && c->route == MING_ROUTE_AUTO && q->N % 4 == 0) {
+      int ks = 256 / tiles;
+      if (ks > (K / 64) / 6) ks = (K / 64) / 6;
+      if (ks >= 2) {
+        split_ks[i] = ks;
+        part_bytes = std::max(part_bytes, (size_t)ks * M * q->N * 4);
+      }
+    }
+    const bool dense_sk =
+        q->bits == 16 && c->route != MING_ROUTE_GENERAL && live_segs[i] == 0 && !o.gate &&
+        !o.yh && tiles < 64 && q->N % 64 == 0 && q->N <= 16 * ming::kMaxGroups &&
+        K % 64 == 0 && o.ldy <= (1 << 30) && (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) &&
+        (uint64_t)q->N * (uint64_t)K * 2 <= (1ull << 32);
+    if (dense_sk) {
+      dense_ks[i] = ming::dense_xa_slices(M, q->N, K);
+      if (dense_ks[i] > 1)
+        part_bytes = std::max(part_bytes, (size_t)dense_ks[i] * M * q->N * 4);
+    }
+    if (o.gate && !fast[i]) up_bytes = std::max(up_bytes, (size_t)M * q->N * 2);
+  }
   // The fast route reads x as fp16 carrying the same (bf16) values: one
   // conversion serves every projection here.
+  const bool need_xh = any_fast && !xh_src;
+  const size_t t_bytes = (size_t)M * t_cols * 2, xh_bytes = need_xh ? (size_t)M * K * 2 : 0;
+
+  // ---- acquire: every scratch region before the first launch ------------
+  uint16_t* T = nullptr;
+  float* part = nullptr;
+  uint16_t* up = nullptr;
   const uint16_t* xh = xh_src;
-  if (any_fast && !xh) {
-    int rc = ensure_xh(c, (size_t)M * K * 2);
+  if (carve) {
+    if (up_bytes > 0) return fail(MING_ERR_ARG, "ming_lin_noalloc: no gated projection");
+    const size_t need = Carve::aligned256(t_bytes) + Carve::aligned256(xh_bytes) +
+                        Carve::aligned256(part_bytes);
+    if (need > carve->cap - carve->used)
+      return fail(MING_ERR_SHAPE,
+                  "ming_lin_noalloc: the call needs " + std::to_string(need) +
+                      " bytes of scratch; the no-alloc array holds " +
+                      std::to_string(carve->cap) + " (MING_NOALLOC_SCRATCH_BYTES)");
+    if (t_bytes) T = (uint16_t*)carve->take(t_bytes);
+    if (xh_bytes) xh = (const uint16_t*)carve->take(xh_bytes);
+    if (part_bytes) part = (float*)carve->take(part_bytes);
+  } else {
+    int rc = MING_OK;
+    if (t_bytes) rc = ensure_scratch(c, t_bytes);
+    if (rc == MING_OK && part_bytes) rc = ensure_part(c, part_bytes);
+    if (rc == MING_OK && xh_bytes) rc = ensure_xh(c, xh_bytes);
+    if (rc == MING_OK && up_bytes) rc = ensure_up(c, up_bytes);
     if (rc != MING_OK) return rc;
-    uint16_t* dst = (uint16_t*)c->xh;
+    if (t_bytes) T = (uint16_t*)c->scratch;
+    if (xh_bytes) xh = (const uint16_t*)c->xh;
+    if (part_bytes) part = (float*)c->part;
+    if (up_bytes) up = (uint16_t*)c->up;
+  }
+
+  // ---- launch ------------------------------------------------------------
+  if (t_cols > 0) {
+    xa.x = x; xa.ldx = ldx; xa.K = K; xa.M = M;
+    xa.n_cols = t_cols; xa.t = T; xa.ldt = t_cols;
+    double a_bytes = 0.0;
+    for (int i = 0; i < n; ++i)
+      if (xa.A[i]) a_bytes += 2.0 * qs[i]->a_rows * (double)K;
+    MING_HIP(profiled(c, kBXa, xa_flops, 2.0 * M * K + a_bytes + 2.0 * M * t_cols,
+                      [&] {
+                        return xa_fast ? ming::launch_lora_xa_fast(xa, part, xa_ks, c->stream)
+                                       : ming::launch_lora_xa(xa, c->stream);
+                      }),
+             "lora_xa launch");
+    c->eng.lora_xa += 1;
+  }
+  if (need_xh) {
+    uint16_t* dst = const_cast<uint16_t*>(xh);
     MING_HIP(profiled(c, kBCvt, 0.0, 4.0 * M * K,
                       [&] { return ming::launch_bf16_to_f16(x, ldx, dst, K, M, K,
                                                             c->stream, range_word(c)); }),
              "bf16->fp16 launch");
-    xh = dst;
   }
   for (int i = 0; i < n; ++i) {
     const ming_qweight* q = qs[i];
@@ -997,28 +1108,15 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     a.yh = nullptr; a.ldyh = 0;
     a.range = range_word(c);
     if (o.gate && !fast[i]) {
-      // the general route writes the projection first: into a plane of its
-      // own, since y may be the gate itself
-      int rc = ensure_up(c, (size_t)M * q->N * 2);
-      if (rc != MING_OK) return rc;
-      a.y = (uint16_t*)c->up; a.ldy = q->N;
+      a.y = up; a.ldy = q->N;
     }
     if (fast[i]) {
       a.x = xh; a.ldx = K; a.codes = q->codes_f; a.sb = q->sbf;
       a.g = o.gate; a.ldg = o.ldg;     // the fast epilogue fuses SwiGLU
       a.yh = o.yh; a.ldyh = q->N;      // and writes the fp16 copy the next projection reads
-      // Few tiles (the context refiner's 256 caption rows: 15 or 40): split
-      // K so about one round of the chip runs, at least 6 K steps a slice
-      const int tiles = ((M + 255) / 256) * ((q->N + 255) / 256);
-      if (tiles < 64 && c->route == MING_ROUTE_AUTO && q->N % 4 == 0) {
-        int ks = 256 / tiles;
-        if (ks > (K / 64) / 6) ks = (K / 64) / 6;
-        if (ks >= 2) {
-          int rc = ensure_part(c, (size_t)ks * M * q->N * 4);
-          if (rc != MING_OK) return rc;
-          a.part = (float*)c->part;
-          a.kslices = ks;
-        }
+      if (split_ks[i] >= 2) {
+        a.part = part;
+        a.kslices = split_ks[i];
       }
     }
     const double base_flops = 2.0 * M * (double)q->N * K;
@@ -1027,32 +1125,17 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
                               : (double)q->N * K * q->bits / 8 + 4.0 * q->N * (K / 64);
     const int bk = fast[i] ? (q->bits == 4 ? kBF4 : kBF8)
                            : (q->bits == 4 ? kBQ4 : (q->bits == 8 ? kBQ8 : kBDense));
-    // A dense weight with no live adapter whose output is a few 256 x 256
-    // tiles (the caption embedder at 256 rows: 15 tiles; the final layer's 64
-    // columns: 16) runs as the x.A path's split-K bf16 GEMM -- identity
-    // column groups, coefficient 1 -- which spreads K over the chip.
-    const bool dense_sk =
-        q->bits == 16 && c->route != MING_ROUTE_GENERAL && live_segs[i] == 0 && !o.gate &&
-        !o.yh && ((M + 255) / 256) * ((q->N + 255) / 256) < 64 && q->N % 64 == 0 &&
-        q->N <= 16 * ming::kMaxGroups && K % 64 == 0 && o.ldy <= (1 << 30) &&
-        (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) &&
-        (uint64_t)q->N * (uint64_t)K * 2 <= (1ull << 32);
-    if (dense_sk) {
-      const int dks = ming::dense_xa_slices(M, q->N, K);
-      if (dks > 1) {
-        int rc = ensure_part(c, (size_t)dks * M * q->N * 4);
-        if (rc != MING_OK) return rc;
-      }
+    if (dense_ks[i] > 0) {
       ming::LoraXaArgs da{};
       da.x = x; da.ldx = ldx; da.A[0] = q->w16; da.K = K; da.M = M;
       da.n_cols = q->N; da.t = o.y; da.ldt = (int)o.ldy;
-      for (int g = 0; g < q->N / 16; ++g) {
-        da.grp[g] = (int16_t)g;
-        da.coef[g] = 1.0f;
+      for (int gi = 0; gi < q->N / 16; ++gi) {
+        da.grp[gi] = (int16_t)gi;
+        da.coef[gi] = 1.0f;
       }
+      const int dks = dense_ks[i];
       MING_HIP(profiled(c, bk, base_flops, 2.0 * M * K + wbytes + 2.0 * M * q->N,
-                        [&] { return ming::launch_lora_xa_fast(da, (float*)c->part, dks,
-                                                               c->stream); }),
+                        [&] { return ming::launch_lora_xa_fast(da, part, dks, c->stream); }),
                "dense split-K launch");
     } else {
       MING_HIP(profiled(c, bk, base_flops + tail_flops[i],
@@ -1067,9 +1150,8 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     if (o.gate && !fast[i]) {
       // the general route writes the projection; SwiGLU follows
       MING_HIP(profiled(c, kBSwiglu, 0.0, 6.0 * M * q->N,
-                        [&] { return ming::launch_swiglu(o.gate, o.ldg, (const uint16_t*)c->up,
-                                                         q->N, o.y, o.ldy, M, q->N,
-                                                         c->stream); }),
+                        [&] { return ming::launch_swiglu(o.gate, o.ldg, up, q->N, o.y,
+                                                         o.ldy, M, q->N, c->stream); }),
                "swiglu launch");
     }
     if (o.gate) c->eng.elementwise += 1;
@@ -1103,6 +1185,27 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
              int64_t ldx, uint16_t* y, int64_t ldy, int M,
              const float* scales) {
   return lin_impl(c, qc, x, ldx, y, ldy, M, scales, nullptr, 0, nullptr, nullptr);
+}
+
+int ming_lin_noalloc(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
+                     int64_t ldx, uint16_t* y, int64_t ldy, int M, const float* scales) {
+  if (!c || !qc) return fail(MING_ERR_ARG, "ming_lin_noalloc: null argument");
+  void* base = noalloc_ptr(c->device);
+  if (!base)
+    return fail(MING_ERR_STATE, "ming_lin_noalloc: the device has no scratch address");
+  Carve cv;
+  cv.base = static_cast<char*>(base);
+  cv.cap = MING_NOALLOC_SCRATCH_BYTES;
+  struct NoEvents {
+    ming_ctx* c;
+    bool was;
+    ~NoEvents() { c->no_events = was; }
+  } ne{c, c->no_events};
+  c->no_events = true;
+  LinOut o;
+  o.y = y;
+  o.ldy = ldy;
+  return lin_multi(c, 1, &qc, &o, x, ldx, M, scales, nullptr, &cv);
 }
 
 int ming_lin_swiglu(ming_ctx* c, const ming_qweight* w, const uint16_t* x,

@@ -64,7 +64,8 @@ def _finalize(obj, _finalizing=sys.is_finalizing):
         pass
 
 
-ERR_RANGE = 7
+ERR_SHAPE, ERR_STATE, ERR_RANGE = 2, 6, 7
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class MingError(RuntimeError):
@@ -202,6 +203,7 @@ def lib():
         "ming_qweight_unbind_lora": ([vp, i32, i32], i32),
         "ming_qweight_lora_rank": ([vp, i32, i32], i32),
         "ming_lin": ([vp, vp, vp, i64, vp, i64, i32, C.POINTER(f32)], i32),
+        "ming_lin_noalloc": ([vp, vp, vp, i64, vp, i64, i32, C.POINTER(f32)], i32),
         "ming_rmsnorm": ([vp, vp, i64, vp, vp, i64, i32, i32, f32], i32),
         "ming_rope_table": ([vp, vp, vp, vp, i32, C.POINTER(i32), i32,
                              C.c_double, vp, vp], i32),
@@ -359,6 +361,14 @@ class Ctx:
         ldy = qw.N if ldy is None else ldy
         _check(lib().ming_lin(self.h, qw.h, _ptr(x), ldx, _ptr(y), ldy, M,
                               _scales(scales)))
+
+    def lin_noalloc(self, qw: "QWeight", x, y, M: int, scales=None, ldx=None,
+                    ldy=None):
+        """ming_lin with the device's static scratch: allocates nothing."""
+        ldx = qw.K if ldx is None else ldx
+        ldy = qw.N if ldy is None else ldy
+        _check(lib().ming_lin_noalloc(self.h, qw.h, _ptr(x), ldx, _ptr(y), ldy, M,
+                                      _scales(scales)))
 
     def lin_swiglu(self, w: "QWeight", x, g, out, M: int, scales=None,
                    ldx=None, ldg=None, ldo=None):
