@@ -114,12 +114,16 @@ def cpu_baseline(hosts, x_host, target_s, threads):
         ffn(rows)
         dt = time.perf_counter() - t0
     base, lora = ffn_flops(rows)
+    cpu = host_cpu()
     return {"value": round((base + lora) / dt / 1e12, 6), "unit": "TFLOP/s",
             "cores": threads, "kind": "port",
             "sample": f"{rows} of {M_TOK} token rows of the same FFN step "
                       f"(w1, w3, swiglu, w2 with the 8 LoRA slots), scalar C "
-                      f"oracle, f64 accumulate, {threads} threads, "
-                      f"{dt:.1f} s"}
+                      f"oracle (f64 accumulation, -O3, no intrinsics), {threads} threads "
+                      f"({cpu['affinity']} cores in the process's affinity, nproc "
+                      f"{cpu['nproc']}), {dt:.1f} s",
+            "cpu_model": cpu["model"], "cpu_mhz": cpu["mhz"], "nproc": cpu["nproc"],
+            "affinity_cores": cpu["affinity"], "accumulate": "f64"}
 
 
 def forward_flops(img, cap, ranks=RANKS, scales=SCALES):
@@ -349,22 +353,81 @@ def time_forward(ctx, m, torch, gen, steps, warmup):
         model.forward(lat, capt, 2560, img, cap, cap, pt, ph, pw, 0.5, out)
         each.append((time.perf_counter() - t0) * 1e3)
     flops = forward_flops(img, cap)
+    return each, flops, model
+
+
+def run_forward1024(ctx, m, torch, gen, steps):
+    """The 1024^2 forward alone: ms per forward (host clock, after two untimed
+    forwards), then the same forwards with the library's per-launch HIP events,
+    summed per kernel family -- the reference's profile buckets
+    (ming-dit.cc:1689-1717) -- as ms and TFLOP/s per forward."""
+    each, flops, model = time_forward(ctx, m, torch, gen, steps, 2)
+    img, cap, grid = 4096, 256, 64
+    import numpy as np
+    pt = np.concatenate([np.full(img, cap + 1), 1 + np.arange(cap)]).astype(np.int32)
+    ph = np.concatenate([np.arange(img) // grid, np.zeros(cap)]).astype(np.int32)
+    pw = np.concatenate([np.arange(img) % grid, np.zeros(cap)]).astype(np.int32)
+    lat = torch.randn((img, 64), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    capt = torch.randn((cap, 2560), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    out = torch.empty((img, 64), dtype=torch.int16, device="cuda")
+    ctx.set_profiling(True)
+    ctx.profile_collect()
+    for _ in range(steps):
+        model.forward(lat, capt, 2560, img, cap, cap, pt, ph, pw, 0.5, out)
+    prof = ctx.profile_collect()
+    ctx.set_profiling(False)
     model.close()
-    return each, flops
+    tot = sum(b["ms"] for b in prof.values())
+    fams = {k: {"ms_per_forward": round(v["ms"] / steps, 3),
+                "launches_per_forward": v["launches"] // steps,
+                "share": round(v["ms"] / tot, 4),
+                "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1) if v["flops"] else None,
+                "gbps": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1) if not v["flops"] else None}
+            for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
+    med = sorted(each)[len(each) // 2]
+    return {"metric": "34-block w4g64 forward @1024^2", "value": round(med, 2), "unit": "ms",
+            "higher_is_better": False, "ms_each": [round(t, 2) for t in each],
+            "tflops": round(flops / (med * 1e-3) / 1e12, 2),
+            "kernel_ms_per_forward": round(tot / steps, 3), "families": fams}
 
 
-def time_norms(ctx, torch, gen, reps=20):
-    """The HBM-bound feeds at configs[3]'s shape (4352 rows, H 3840, 30 heads):
+def time_forward_2048(model, torch, gen, steps):
+    """configs[3] on an already-built model (the same 34 blocks and adapters
+    as the 1024^2 forward): ms per 2048^2 forward after one untimed one."""
+    img, cap, pos = layout_2048()
+    lat = torch.randn((img, 64), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    capt = torch.randn((cap, 2560), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    out = torch.empty((img, 64), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()
+    model.forward(lat, capt, 2560, img, cap, cap, *pos, 0.5, out)
+    each = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        model.forward(lat, capt, 2560, img, cap, cap, *pos, 0.5, out)
+        each.append((time.perf_counter() - t0) * 1e3)
+    return each, forward_flops(img, cap)
+
+
+def time_norms(ctx, torch, gen, rounds=4):
+    """The HBM-bound feeds at configs[2]'s shape (4352 rows, H 3840, 30 heads):
     RMSNorm [4352, 3840] out of place, and qk-norm + RoPE in place on the
-    token-major [4352, 3*3840] qkv plane. Per-launch HIP events; achieved =
-    algorithmic bytes (activations read + written once, gains; the rotary
-    tables excluded) / average launch time, against 8 TB/s."""
+    token-major [4352, 3*3840] qkv plane. Each kernel walks a ring of
+    buffers totalling more than the 256 MB Infinity Cache (MALL), so every
+    launch reads its input from HBM, not from a cache the previous launch
+    filled; the launches of a round are bracketed by two events on the
+    context's stream. achieved = algorithmic bytes (activations read + written
+    once, gains; the rotary tables excluded) / average launch time, against
+    8 TB/s."""
     import numpy as np
     rows, H, NH = M_TOK, HID, HID // 128
-    x = torch.randn((rows, H), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
-    y = torch.empty_like(x)
+    n_rms = 6                      # 6 x (33.4 MB in + 33.4 MB out) = 401 MB
+    n_qk = 4                       # 4 x 100.3 MB qkv planes = 401 MB
+    xs = [torch.randn((rows, H), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+          for _ in range(n_rms)]
+    ys = [torch.empty_like(xs[0]) for _ in range(n_rms)]
     w = (1.0 + 0.1 * torch.randn((H,), generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
-    qkv = torch.randn((rows, 3 * H), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    qkvs = [torch.randn((rows, 3 * H), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+            for _ in range(n_qk)]
     nq = (1.0 + 0.1 * torch.randn((128,), generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
     nk = (1.0 + 0.1 * torch.randn((128,), generator=gen, device="cuda")).to(torch.bfloat16).view(torch.int16)
     img, cap, grid = 4096, 256, 64
@@ -374,28 +437,62 @@ def time_norms(ctx, torch, gen, reps=20):
     cos_t = torch.empty((rows, 64), dtype=torch.float32, device="cuda")
     sin_t = torch.empty_like(cos_t)
     ctx.rope_table(pt, ph, pw, rows, cos_t, sin_t)
-    for _ in range(3):
-        ctx.rmsnorm(x, w, y, rows, H)
-        ctx.qk_norm_rope(qkv, 3 * H, 0, H, rows, NH, nq, nk, cos_t, sin_t)
-    ctx.synchronize()
-    ctx.set_profiling(True)
-    ctx.profile_collect()
-    for _ in range(reps):
-        ctx.rmsnorm(x, w, y, rows, H)
-        ctx.qk_norm_rope(qkv, 3 * H, 0, H, rows, NH, nq, nk, cos_t, sin_t)
-    ctx.synchronize()
-    prof = ctx.profile_collect()
-    ctx.set_profiling(False)
+    cstream = torch.cuda.ExternalStream(ctx_stream(ctx))
+
+    def run_rms(i):
+        ctx.rmsnorm(xs[i % n_rms], w, ys[i % n_rms], rows, H)
+
+    def run_qk(i):
+        ctx.qk_norm_rope(qkvs[i % n_qk], 3 * H, 0, H, rows, NH, nq, nk, cos_t, sin_t)
+
     out = {}
-    for k, shape in (("rmsnorm", [rows, H]), ("qk_norm_rope", [rows, 2 * H])):
-        b = prof[k]
-        gbps = b["bytes"] / (b["ms"] * 1e-3) / 1e9
-        out[k] = {"shape": shape, "launches": b["launches"],
-                  "avg_us": round(1e3 * b["ms"] / b["launches"], 2),
-                  "bytes_per_launch": round(b["bytes"] / b["launches"]),
-                  "achieved_gbps": round(gbps, 1), "peak_gbps": 8000.0,
-                  "frac": round(gbps / 8000.0, 4)}
+    for name, fn, nbuf, shape, nbytes, ring in (
+            ("rmsnorm", run_rms, n_rms, [rows, H], 4.0 * rows * H + 2.0 * H,
+             n_rms * 4 * rows * H),
+            ("qk_norm_rope", run_qk, n_qk, [rows, 2 * H], 8.0 * rows * H + 512.0,
+             n_qk * 6 * rows * H)):
+        for i in range(2 * nbuf):                 # warm: every buffer touched
+            fn(i)
+        ctx.synchronize()
+        n = rounds * nbuf
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(cstream)
+        for i in range(n):
+            fn(i)
+        e1.record(cstream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"shape": shape, "launches": n, "ring_bytes": int(ring),
+                     "avg_us": round(us, 2), "bytes_per_launch": round(nbytes),
+                     "achieved_gbps": round(gbps, 1), "peak_gbps": PEAK_HBM_GBS,
+                     "frac": round(gbps / PEAK_HBM_GBS, 4)}
     return out
+
+
+def ctx_stream(ctx):
+    """The context's HIP stream handle (an int)."""
+    import ming_dit_amd as m
+    return int(m.lib().ming_ctx_stream(ctx.h) or 0)
+
+
+def host_cpu():
+    """The host's CPU as the baseline ran on it: model, clock, counts."""
+    info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "model": None, "mhz": None}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k == "model name" and info["model"] is None:
+                    info["model"] = v.strip()
+                elif k == "cpu MHz" and info["mhz"] is None:
+                    info["mhz"] = float(v)
+    except OSError:
+        pass
+    return info
 
 
 TRAFFIC_MD = os.path.join(ROOT, "profiles", "qproj_w4_ffn_config2_traffic.md")
@@ -424,11 +521,15 @@ def main():
                     help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-forward", action="store_true",
-                    help="skip the 34-block forward at 1024^2")
+                    help="skip the 34-block forwards (1024^2 and 2048^2)")
+    ap.add_argument("--no-cfg", action="store_true",
+                    help="skip configs[4] (the CFG x 2 w8 denoise at 2048^2)")
     ap.add_argument("--forward-steps", type=int, default=5)
-    ap.add_argument("--workload", choices=("ffn", "forward2048", "cfg2048"), default="ffn",
-                    help="ffn: the headline line (configs[1] + the 1024^2 forward); "
-                         "forward2048: configs[3]; cfg2048: configs[4]")
+    ap.add_argument("--workload", choices=("ffn", "forward1024", "forward2048", "cfg2048"),
+                    default="ffn",
+                    help="ffn: the headline line (configs[1], the forwards, configs[4]); "
+                         "forward1024: the 1024^2 forward alone, with its kernel-family "
+                         "breakdown; forward2048: configs[3]; cfg2048: configs[4]")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB device-to-device three times (the "
                          "known-size kernel the HBM byte counters are scaled by)")
@@ -455,6 +556,11 @@ def main():
     stream = torch.cuda.Stream()
     ctx = m.Ctx(0, stream.cuda_stream)
     gen = torch.Generator(device="cuda").manual_seed(2)
+    if args.workload == "forward1024":
+        res = run_forward1024(ctx, m, torch, gen, args.forward_steps)
+        ctx.close()
+        print(json.dumps(res))
+        return
     if args.workload != "ffn":
         fn = run_forward2048 if args.workload == "forward2048" else run_cfg2048
         res = fn(ctx, m, torch, gen, args.forward_steps) if args.workload == "forward2048" \
@@ -552,17 +658,33 @@ def main():
         # ~110 ms); the timed ones are reported one by one, with their median
         # as the figure: an occasional forward on these boxes takes ~40 ms
         # longer, and the list shows when one did
-        each, fflops = time_forward(ctx, m, torch, gen, args.forward_steps, 2)
+        each, fflops, model = time_forward(ctx, m, torch, gen, args.forward_steps, 2)
         fms = sorted(each)[len(each) // 2]
         out["forward_ms_1024"] = round(fms, 2)
         out["forward_ms_mean"] = round(sum(each) / len(each), 2)
         out["forward_ms_each"] = [round(t, 2) for t in each]
         out["forward_tflops_1024"] = round(fflops / (fms * 1e-3) / 1e12, 2)
         out["forward_tflop"] = round(fflops / 1e12, 2)
+        # the same model at 2048^2 (16384 image + 256 caption tokens)
+        each2, fflops2 = time_forward_2048(model, torch, gen, 3)
+        model.close()
+        fms2 = sorted(each2)[len(each2) // 2]
+        out["forward_ms_2048"] = round(fms2, 2)
+        out["forward_ms_2048_each"] = [round(t, 2) for t in each2]
+        out["forward_tflops_2048"] = round(fflops2 / (fms2 * 1e-3) / 1e12, 2)
+    if not args.no_cfg:
+        # CFG x 2, w8, eight r64 slots, 11 denoise steps at 2048^2
+        cfg = run_cfg2048(ctx, m, torch, gen)
+        out["cfg2048_tflops_sustained"] = cfg["value"]
+        out["cfg2048_ms_per_forward_median"] = cfg["ms_per_forward_median"]
+        out["cfg2048_ms_per_step_each"] = cfg["ms_per_step_each"]
+        out["cfg2048_finite"] = cfg["finite"]
     if not args.no_cpu:
         import numpy as np
         xh = x.cpu().view(torch.int16).numpy().view(np.uint16)
-        threads = min(16, os.cpu_count() or 1)
+        # every core of the process's affinity, up to the one-GPU box's CPU
+        # share of 16
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
         out["cpu_baseline"] = cpu_baseline(hosts, xh, args.cpu_seconds, threads)
     ctx.close()
     print(json.dumps(out))
