@@ -424,6 +424,82 @@ def test_few_tiles_ffn_equals_the_four_calls(ctx):
         wt.close()
 
 
+# The stacked x.A over thousands of rows: stacked widths of 64 to 896
+# columns (half-filled 128-column blocks included), ragged row counts, and K
+# of one to three 64-wide steps (fewer than the stage ring holds).
+MANY_ROWS_XA_CASES = [
+    (2085, 256, 192, [16], [0.7]),
+    (2085, 256, 192, [128, 64, 32, 16, 8, 4], [0.3, -0.5, 1.1, 0.9, 0.0, 1.4]),
+    (4352, 256, 192, list(CFG2_RANKS), list(CFG2_SCALES)),
+    (4300, 256, 128, [128, 128, 128, 128, 64], [0.4, -0.2, 0.0, 0.3, 1.0]),
+    (4300, 256, 64, [128] * 7, [0.2, -0.3, 0.25, 0.0, 0.15, -0.1, 0.3]),
+]
+
+
+@pytest.mark.parametrize("M,N,K,ranks,scales", MANY_ROWS_XA_CASES)
+def test_many_rows_xa_parity(ctx, orc, M, N, K, ranks, scales):
+    """One projection with up to seven live adapters over 2085-4352 rows
+    against the oracle."""
+    print(f"case many-rows x.A M={M} N={N} K={K} ranks={ranks}", flush=True)
+    x = bf16(randn(3000 + M + K, (M, K)))
+    pack, w = make_weight(3001 + len(ranks), N, K, 4)
+    qw = _qw(ctx, pack, 4)
+    loras = []
+    for s, r in enumerate(ranks):
+        A, B = make_lora(3100 + 2 * s, N, K, r)
+        qw.bind_lora(s, A, B)
+        loras.append((A, B, scales[s]))
+    sc = list(scales) + [0.0] * (8 - len(scales))
+    ctx.reset_engagement()
+    y = _run(ctx, qw, to_dev(x), M, sc)
+    eng = ctx.engagement()
+    assert eng["lora_xa"] == 1 and eng["lora_proj"] == 1
+    ref = orc.proj(x, w, loras)
+    assert _rel(orc, y, ref) <= TOL
+    assert orc.rel_l2(ref, orc.proj(x, w)) > 10 * TOL
+    qw.close()
+
+
+def test_many_rows_xa_stacking_moves_no_bits(ctx):
+    """Over 2085 rows q|k|v fused (768 stacked T columns) gives the bits of
+    the three projections run alone (256 columns each), and ming_ffn (w1|w3
+    stacked) the bits of the four calls."""
+    M, H, K = 2085, 256, 256
+    x = to_dev(bf16(randn(3201, (M, K))))
+    parts = []
+    for i in range(3):
+        pack, _ = make_weight(3202 + i, H, K, 4)
+        p = _qw(ctx, pack, 4)
+        for s in range(2):
+            A, B = make_lora(3210 + 4 * i + 2 * s, H, K, 128)
+            p.bind_lora(s, A, B)
+        parts.append(p)
+    fused = m.QWeight.concat(ctx, parts)
+    sc = [0.8, -0.6]
+    yf = _run(ctx, fused, x, M, sc)
+    for i, p in enumerate(parts):
+        assert np.array_equal(yf[:, i * H:(i + 1) * H], _run(ctx, p, x, M, sc))
+    for p in parts + [fused]:
+        p.close()
+
+    Hf, F = 384, 640
+    w1, w3, w2 = _ffn_weights(ctx, 3220, Hf, F)
+    x = to_dev(bf16(randn(3221, (M, Hf))))
+    g = to_dev(_run(ctx, w1, x, M, CFG2_SCALES))
+    u = to_dev(_run(ctx, w3, x, M, CFG2_SCALES))
+    a = empty_bf16(M, F)
+    sync()
+    ctx.swiglu(g, u, a, M, F)
+    sync()
+    ref = _run(ctx, w2, a, M, CFG2_SCALES)
+    y = empty_bf16(M, Hf)
+    ctx.ffn(w1, w3, w2, x, y, M, CFG2_SCALES)
+    sync()
+    assert np.array_equal(from_dev(y), ref)
+    for wt in (w1, w3, w2):
+        wt.close()
+
+
 def orc_f32(v):
     return (v.astype(np.uint32) << 16).view(np.float32)
 
