@@ -512,6 +512,49 @@ def measured_traffic():
     return None
 
 
+def mfma_ceiling(torch, seconds=2.0, variants=("f16_random", "bf16_random", "f16_zero")):
+    """The sustained MFMA rate of a kernel that does nothing else (see
+    vpipe-ming-image_amd/calib/mfma_ceiling.hip): per variant, launches of
+    ~25 ms back to back for about `seconds`, the median of the second half."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                   "vpipe-ming-image_amd", "libming_calib.so"))
+    lib.ming_calib_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = torch.cuda.Stream()
+    out = torch.empty(cus * 256, dtype=torch.float32, device="cuda")
+    iters = 50000
+    flop = cus * 4 * iters * 16 * 32768.0
+    res = {"metric": "mfma_ceiling", "unit": "TFLOP/s", "cus": cus, "blocks": cus,
+           "iters_per_launch": iters, "flop_per_launch": flop,
+           "peak_nominal_tflops": {"f16": 2516.6, "bf16": 2516.6}}
+    for name, bf16, zero in (("f16_random", 0, 0), ("bf16_random", 1, 0), ("f16_zero", 0, 1)):
+        if name not in variants:
+            continue
+        times = []
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(times) < 6:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            rc = lib.ming_calib_mfma(bf16, cus, iters, zero, 12345 + len(times),
+                                     out.data_ptr(), ctypes.c_void_p(stream.cuda_stream))
+            assert rc == 0, rc
+            e1.record(stream)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1))
+        late = sorted(times[len(times) // 2:])
+        ms = late[len(late) // 2]
+        tf = flop / (ms * 1e-3) / 1e12
+        res[name] = {"ms_per_launch": round(ms, 3), "tflops": round(tf, 1),
+                     "launches": len(times),
+                     # the clock at which 1024 FLOP/clk per SIMD gives this rate
+                     "equiv_ghz": round(tf * 1e12 / (cus * 4 * 1024) / 1e9, 3)}
+        assert torch.isfinite(out).all()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -530,6 +573,10 @@ def main():
                     help="ffn: the headline line (configs[1], the forwards, configs[4]); "
                          "forward1024: the 1024^2 forward alone, with its kernel-family "
                          "breakdown; forward2048: configs[3]; cfg2048: configs[4]")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="measure the MFMA throughput this board sustains under its power "
+                         "limit: back-to-back 32x32x16 f16/bf16 MFMAs on register operands, "
+                         "the projection kernels' occupancy, random and zero operands")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB device-to-device three times (the "
                          "known-size kernel the HBM byte counters are scaled by)")
@@ -541,6 +588,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.mfma_ceiling:
+        print(json.dumps(mfma_ceiling(torch)))
+        return
     if args.copy_calibration:
         n = 256 * 1024 * 1024 // 4
         src = torch.randint(0, 1 << 30, (n,), dtype=torch.int32, device="cuda")
@@ -652,6 +702,15 @@ def main():
     }
     for w in (w1, w3, w2):
         w.close()
+    # the MFMA rate this board sustains on random fp16 operands under its
+    # power limit (the projection's own MFMA type and occupancy), measured
+    # here so the fraction below compares two numbers from one box
+    ceil = mfma_ceiling(torch, seconds=1.0, variants=("f16_random",))["f16_random"]
+    out["roofline"]["measured_ceiling"] = {
+        "what": "back-to-back fp16 32x32x16 MFMAs on random register operands, one "
+                "256-thread block per CU (bench.py --mfma-ceiling)",
+        "tflops": ceil["tflops"], "equiv_ghz": ceil["equiv_ghz"],
+        "frac": round(achieved / ceil["tflops"], 4)}
     out["hbm_kernels"] = time_norms(ctx, torch, gen)
     if not args.no_forward:
         # two untimed forwards (the first allocates the forward's workspaces,

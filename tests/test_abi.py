@@ -56,3 +56,13 @@ def test_context_on_a_missing_device_is_an_error_not_a_crash():
             assert e.code in (1, 3)
         else:
             raise AssertionError("a context without a GPU must be refused")
+
+
+def test_calibration_library_exports_its_entry_point():
+    """bench.py --mfma-ceiling loads libming_calib.so (built beside the
+    library, outside its ABI) and calls ming_calib_mfma."""
+    import os
+    path = os.path.join(os.path.dirname(m.LIB_PATH), "libming_calib.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", path],
+                         capture_output=True, text=True, check=True).stdout
+    assert " T ming_calib_mfma" in out
