@@ -128,6 +128,27 @@ def test_attention_full_size_properties(ctx):
     assert np.all(g <= vmax[None] * (1 + 2 ** -7) + 1e-6)
 
 
+def test_attention_full_size_against_fp32_reference(ctx):
+    """30 heads x 4352 rows (configs[2]'s attention) against the torch fp32
+    reference (per-head softmax(q k^T * scale) v in fp32; pinned to the
+    oracle in test_torch_ref.py), at the oracle's bar."""
+    import torch
+    from torch_ref import Ref
+    rows, heads = 4352, 30
+    qkv, q, k, v = qkv_problem(23, rows, heads)
+    got = f32(run(ctx, qkv, rows, heads))
+    ref = Ref("f32", "cuda")
+    t = lambda a: torch.from_numpy(f32(a)).cuda()
+    want = ref.attention(t(q), t(k), t(v), heads, 1.0 / np.sqrt(128)).cpu().numpy()
+    rel = orc.rel_l2(got, want)
+    print(f"4352 x 30 heads vs fp32 reference: rel-L2 {rel:.2e}", flush=True)
+    assert rel <= TOL
+    # per head, too: no head may hide behind the others
+    g, w_ = got.reshape(rows, heads, 128), want.reshape(rows, heads, 128)
+    for h in range(heads):
+        assert orc.rel_l2(g[:, h], w_[:, h]) <= TOL, h
+
+
 def test_attention_rejects_bad_shapes(ctx):
     import ming_dit_amd as m
     rows, heads = 64, 1
