@@ -87,3 +87,38 @@ def test_model_rejects_bad_layout(ctx):
         model.forward(ld, cd, cs, img, CAP, CAP + 1, lay["pos_t"], lay["pos_h"],
                       lay["pos_w"], 0.5, out)
     model.close()
+
+
+def test_caption_cache_follows_direct_rebinding(ctx):
+    """Binding or unbinding an adapter directly on a borrowed context-refiner
+    weight (not through the model) is never answered from the caption cache:
+    the next forward refines the caption again, with the binding in force,
+    and gives the bits of an uncached forward."""
+    from helpers import make_lora
+    mo, model = build_model(ctx, 9)
+    for i, s in enumerate(SCALES):
+        model.set_lora_scale(i, s)
+    lay, img, lat, cap, cs = inputs()
+    ctx.reset_engagement()
+    a = run(model, lay, img, lat, cap, cs, 0.6)
+    assert np.array_equal(run(model, lay, img, lat, cap, cs, 0.6), a)
+    assert ctx.engagement()["cap_cache_hits"] == 1
+    w1 = model._keep[0]["w1"]              # the context refiner's w1, borrowed
+    A, B = make_lora(901, w1.N, w1.K, 16)
+    w1.bind_lora(0, A, B)                  # slot 0 is live (strength 1)
+    rebound = run(model, lay, img, lat, cap, cs, 0.6)
+    assert ctx.engagement()["cap_cache_hits"] == 1
+    assert not np.array_equal(rebound, a)
+    model.set_caption_cache(False)
+    assert np.array_equal(run(model, lay, img, lat, cap, cs, 0.6), rebound)
+    model.set_caption_cache(True)
+    assert np.array_equal(run(model, lay, img, lat, cap, cs, 0.6), rebound)
+    assert ctx.engagement()["cap_cache_hits"] == 1     # refilled, not hit
+    assert np.array_equal(run(model, lay, img, lat, cap, cs, 0.6), rebound)
+    assert ctx.engagement()["cap_cache_hits"] == 2     # now cached
+    w1.unbind_lora(0)
+    unbound = run(model, lay, img, lat, cap, cs, 0.6)
+    assert ctx.engagement()["cap_cache_hits"] == 2
+    model.set_caption_cache(False)
+    assert np.array_equal(run(model, lay, img, lat, cap, cs, 0.6), unbound)
+    model.close()

@@ -55,6 +55,8 @@ struct ming_model {
     void* out = nullptr;  // the context-refined rows [len][H]
     size_t out_cap = 0;
     uint64_t tick = 0;
+    // the caption path's weights' bind generations when it was filled
+    uint64_t bind_sig = 0;
   };
   bool cap_cache_on = true;
   CapEntry cap[2];

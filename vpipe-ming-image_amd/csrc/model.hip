@@ -259,17 +259,29 @@ bool grow(void** p, size_t* cap, size_t bytes) {
   return true;
 }
 
-// The caption-cache entry holding exactly these caption bytes, or null
-// (ming-dit.cc:1543-1560): shape fields first, then the bytes, compared on
-// the device.
+// The context refiner's adapter state: the sum of its projections' bind
+// generations, which grows with every bind or unbind of any of them (through
+// ming_model_bind_loras or directly on a borrowed weight).
+uint64_t caption_bind_sig(const ming_model* m) {
+  uint64_t sig = 0;
+  for (const ming_block_desc& b : m->ctx_blocks)
+    for (const ming_qweight* q : {b.q, b.k, b.v, b.o, b.w1, b.w3, b.w2})
+      sig += ming::rt_qweight_bind_gen(q);
+  return sig;
+}
+
+// The caption-cache entry holding exactly these caption bytes, refined with
+// the current adapter bindings, or null (ming-dit.cc:1543-1560): shape fields
+// and binding signature first, then the bytes, compared on the device.
 int cap_lookup(ming_model* m, const uint16_t* cap, int CAP, int Q, int64_t stride,
-               hipStream_t s, ming_model::CapEntry** hit) {
+               uint64_t sig, hipStream_t s, ming_model::CapEntry** hit) {
   *hit = nullptr;
   const size_t bytes = (size_t)CAP * (size_t)stride * 2;
   int cand[2], nc = 0;
   for (int i = 0; i < 2; ++i) {
     const ming_model::CapEntry& e = m->cap[i];
-    if (e.valid && e.q == Q && e.len == CAP && e.stride == stride && e.key_bytes == bytes)
+    if (e.valid && e.q == Q && e.len == CAP && e.stride == stride && e.key_bytes == bytes &&
+        e.bind_sig == sig)
       cand[nc++] = i;
   }
   if (nc == 0) return MING_OK;
@@ -603,8 +615,9 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
   ming_model::CapEntry* fill = nullptr;
   const size_t cap_bytes = (size_t)CAP * (size_t)cap_stride * 2;
   const bool cacheable = m->cap_cache_on && reinterpret_cast<uintptr_t>(cap) % 16 == 0;
+  const uint64_t bind_sig = caption_bind_sig(m);
   if (cacheable) {
-    RC(cap_lookup(m, cap, CAP, Q, cap_stride, s, &hit));
+    RC(cap_lookup(m, cap, CAP, Q, cap_stride, bind_sig, s, &hit));
     if (!hit) {
       fill = &m->cap[0];
       for (auto& e : m->cap) {
@@ -736,6 +749,7 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
     fill->len = CAP;
     fill->stride = cap_stride;
     fill->key_bytes = cap_bytes;
+    fill->bind_sig = bind_sig;
     fill->tick = ++m->cap_tick;
   }
   return rt_ok();

@@ -27,6 +27,8 @@ int rt_alloc(ming_ctx* c, size_t bytes, bool zero, void** dev);
 int rt_h2d(ming_ctx* c, void* dev, const void* host, size_t bytes);
 int rt_d2h(ming_ctx* c, void* host, const void* dev, size_t bytes);
 void rt_note_cap_hit(ming_ctx* c);
+// a weight's bind generation (bumped by every ming_qweight_bind_lora / unbind)
+uint64_t rt_qweight_bind_gen(const ming_qweight* q);
 // After the stream has drained: MING_ERR_RANGE (counted, reason set, word
 // cleared) when an fp16 copy met a value it cannot hold since the last check.
 int rt_take_range_fault(ming_ctx* c, const char* who);

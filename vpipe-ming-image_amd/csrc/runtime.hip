@@ -174,6 +174,10 @@ struct ming_qweight {
   int a_rows = 0;            // rows of A_all
   std::vector<int> b_col0;   // [seg*8 + slot] column in B_seg[seg]
   std::vector<int> b_ld;     // per segment: R16 of the segment
+  // bumped by every bind and unbind: a model's caption cache keys on the
+  // context-refiner weights' generations, so a direct rebinding of one of
+  // them is never served stale rows
+  uint64_t bind_gen = 0;
 };
 
 namespace {
@@ -778,6 +782,7 @@ int ming_qweight_bind_lora(ming_qweight* q, int segment, int slot, int rank,
   if (old.B) (void)hipFree(old.B);
   old = nb;
   q->stacks_dirty = true;
+  ++q->bind_gen;
   return ok();
 }
 
@@ -793,6 +798,7 @@ int ming_qweight_unbind_lora(ming_qweight* q, int segment, int slot) {
   if (b.B) (void)hipFree(b.B);
   b = LoraBind{};
   q->stacks_dirty = true;
+  ++q->bind_gen;
   return ok();
 }
 
@@ -1683,6 +1689,7 @@ void rt_free(ming_ctx* c, void* dev) {
 }
 
 void rt_note_cap_hit(ming_ctx* c) { c->eng.cap_cache_hits += 1; }
+uint64_t rt_qweight_bind_gen(const ming_qweight* q) { return q ? q->bind_gen : 0; }
 
 int rt_take_range_fault(ming_ctx* c, const char* who) {
   DeviceGuard dg(c->device);
