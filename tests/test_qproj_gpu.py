@@ -73,7 +73,7 @@ def test_base_projection_parity(ctx, orc, bits, M, N, K):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("M,N,K", [(320, 768, 1024), (520, 8192, 512)])
 def test_lora_eight_slots_parity(ctx, orc, bits, M, N, K):
-    """BASELINE config 2's adapter set on one projection (a 9-chunk LoRA
+    """BASELINE config 2's adapter set on one projection (an 8-chunk LoRA
     tail): on a few tiles (6: the fast route splits K) and on a grid of 96
     tiles with a ragged last tile-row (the unsplit fast kernel)."""
     print(f"case eight slots bits={bits} M={M} N={N} K={K}", flush=True)
@@ -99,6 +99,36 @@ def test_lora_eight_slots_parity(ctx, orc, bits, M, N, K):
     assert rel <= TOL
     # the adapter MOVED the output far past the bar (not a vacuous match)
     assert orc.rel_l2(ref, base) > 10 * TOL
+
+
+ODD_RANKS = (3, 12, 20, 5, 36, 1, 7, 9)
+ODD_SCALES = (0.9, -0.6, 0.4, 1.3, 0.25, -1.1, 0.0, 0.7)
+
+
+@pytest.mark.parametrize("M,N,K", [(2085, 2048, 256), (300, 768, 1024)])
+def test_ranks_off_the_group_grid_parity(ctx, orc, M, N, K):
+    """Ranks that are no multiple of the 8-rank packing group, so zero rows
+    pad groups in the middle of the stack and a slot's groups straddle the
+    tails' 32-rank chunks: on an unsplit grid (72 tiles) and a split one."""
+    print(f"case odd ranks M={M} N={N} K={K}", flush=True)
+    x = bf16(randn(41 + M, (M, K)))
+    pack, w = make_weight(42, N, K, 4)
+    qw = _qw(ctx, pack, 4)
+    loras = []
+    for s, r in enumerate(ODD_RANKS):
+        A, B = make_lora(300 + 2 * s, N, K, r)
+        qw.bind_lora(s, A, B)
+        loras.append((A, B, ODD_SCALES[s]))
+    ctx.reset_engagement()
+    y = _run(ctx, qw, to_dev(x), M, ODD_SCALES)
+    eng = ctx.engagement()
+    assert eng["lora_proj"] == 1 and eng["lora_xa"] == 1
+    tiles = ((M + 255) // 256) * ((N + 255) // 256)
+    assert eng["gemm_split"] == (1 if route_is_auto(ctx) and tiles < 64 else 0)
+    ref = orc.proj(x, w, loras)
+    assert _rel(orc, y, ref) <= TOL
+    assert orc.rel_l2(ref, orc.proj(x, w)) > 10 * TOL
+    qw.close()
 
 
 def test_zero_strength_is_bit_identical(ctx, orc):
@@ -520,7 +550,7 @@ def test_config2_ffn_full_size(ctx, orc):
     the eight slots {4, 8, 16, 16, 32, 32, 64, 128} at strengths
     {1, .5, 0, -.3, .8, 0, 1.2, .25} on all three, through ming_ffn (the
     bench's step). 17 x 40 = 680 tiles: the unsplit w4 kernel with the
-    9-chunk tail and, on w3, the fused SwiGLU epilogue. On a row sample over
+    8-chunk tail and, on w3, the fused SwiGLU epilogue. On a row sample over
     all 17 M tiles, against the oracle (gpu_ff, ming-dit.cc:2151-2162):
       h (w3's fused epilogue) vs swiglu(bf16(x.W1'), bf16(x.W3')) and y vs
       the f32 reference of w2 on the kernel's own h: each stage on its own

@@ -40,7 +40,7 @@ def test_noalloc_matches_ming_lin_on_calls_that_shrink(ctx):
     import torch
     ctx.set_route("auto")
     cases = [  # (M, N, K, bits, ranks, scales): each smaller than the last
-        (4352, 10240, 3840, 4, CFG2_RANKS, CFG2_SCALES),       # 680 tiles, 9-chunk tail
+        (4352, 10240, 3840, 4, CFG2_RANKS, CFG2_SCALES),       # 680 tiles, 8-chunk tail
         (300, 512, 640, 8, (16, 64), (0.7, -0.4)),             # ragged, two slots
         (256, 3840, 3840, 4, CFG2_RANKS, CFG2_SCALES),         # 15 tiles: split K
     ]

@@ -19,11 +19,11 @@ namespace ming {
 //   bits 16: dense bf16 w[n][k] (the checkpoint's own layout)
 //   sb[kt][n] = bf16 scale | bf16 bias << 16 (bits 4 and 8)
 // T is the LoRA intermediate [M][ldt] bf16 (already scaled), B the
-// segment's factors [N_seg][ldb] bf16, gathered per 16-wide rank group by
-// `grp` (B column / 16, or -1 for a zero group).
+// segment's factors [N_seg][ldb] bf16, gathered per 8-wide rank group by
+// `grp` (B column / 8, or -1 for a zero group).
 constexpr int kQpBM = 256, kQpBN = 256, kQpBK = 64, kQpThreads = 256;
 constexpr int kMaxSeg = 4;
-constexpr int kMaxGroups = 256;   // 16-wide rank groups per call
+constexpr int kMaxGroups = 512;   // 8-wide rank groups per call (4096 ranks)
 
 struct QprojSeg {
   int n_begin;          // first output column of this segment
@@ -110,7 +110,7 @@ constexpr int kMaxXaSources = 4;
 struct LoraXaArgs {
   const uint16_t* x;
   long long ldx;
-  // A stacks [rows][K]: group entry g reads rows 16 * (g & 4095) + 0..15 of
+  // A stacks [rows][K]: group entry g reads rows 8 * (g & 4095) + 0..7 of
   // A[g >> 12]; a negative entry is a zero (padding) group
   const uint16_t* A[kMaxXaSources];
   int K;

@@ -258,8 +258,8 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
       xr[i] = in ? *reinterpret_cast<const uint4*>(a.t + (long long)m * a.ldt + tc)
                  : make_uint4(0, 0, 0, 0);
     }
-    const int g = in ? a.grp[grp0 + ch * 4 + (pc >> 1)] : -1;
-    const int bc = (g < 0 ? 0 : g * 16) + (pc & 1) * 8;
+    const int g = in ? a.grp[grp0 + ch * 8 + pc] : -1;
+    const int bc = g < 0 ? 0 : g * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       int n = n0 + pr + 32 * i;
@@ -394,11 +394,11 @@ __global__ __launch_bounds__(256, 2) void lora_xa_kernel(const LoraXaArgs a) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int c = c0 + pr + 32 * i;
-    const int g = a.grp[c >> 4];
+    const int g = a.grp[c >> 3];
     azero[i] = g < 0;
     // a padding group reads (and zeroes) rows of the first live group's stack
     const int gs = g < 0 ? a.grp[0] : g;
-    arow[i] = a.A[gs >> 12] + (long long)(g < 0 ? 0 : (16 * (g & 4095) + (c & 15))) * a.K +
+    arow[i] = a.A[gs >> 12] + (long long)(g < 0 ? 0 : (8 * (g & 4095) + (c & 7))) * a.K +
               pc * 8;
   }
   uint4 xr[4], ar[2];
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(256, 2) void lora_xa_kernel(const LoraXaArgs a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int c = c0 + 32 * j + 8 * q + 4 * fk;
-      const float f = a.coef[c >> 4];
+      const float f = a.coef[c >> 3];
       uint2 v;
       v.x = pack_bf16x2_rne(f * acc[j][4 * q + 0], f * acc[j][4 * q + 1]);
       v.y = pack_bf16x2_rne(f * acc[j][4 * q + 2], f * acc[j][4 * q + 3]);

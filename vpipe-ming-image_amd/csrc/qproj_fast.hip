@@ -405,8 +405,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     const uint16_t* __restrict__ Bp = a.seg[sg].B;
     // the first live group of the segment: a finite source for padding
     // groups (their T columns are exactly 0)
-    const int g_safe =
-        (int16_t)(reinterpret_cast<const uint32_t*>(a.grp)[grp0 >> 1] & 0xffffu);
+    const int g_safe = a.grp[grp0];
     uint32_t toff[4];
     uint32_t boff[4];
     int bc[4];
@@ -420,28 +419,30 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
       toff[i] = (uint32_t)(((long long)m * a.ldt + t_col0 + 8 * c) * 2);
       int n = n0 + row;
       n = n < seg_ne - 1 ? n : seg_ne - 1;
-      boff[i] = (uint32_t)(((long long)(n - seg_nb) * ldb + 8 * (c & 1)) * 2);
+      boff[i] = (uint32_t)((long long)(n - seg_nb) * ldb * 2);
       bc[i] = c;
     }
-    // T region = first 16 KB of the stage buffer, B region = second. The
-    // two 16-rank groups of a chunk are wave-uniform (scalar loads).
+    // T region = first 16 KB of the stage buffer, B region = second. A
+    // lane's 16 bytes are the 8 ranks of one group; the chunk's four groups
+    // are wave-uniform (scalar loads).
     auto issue_t = [&](int ch, const uint4* X) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         dma16_sb(a.t + 32 * ch, toff[i], lds_addr(X + 64 * (4 * wave + i)));
-      // The chunk's two groups are one aligned dword of the table (a
-      // segment's groups start at a multiple of 2): a wave-uniform scalar
+      // The chunk's four groups are one aligned 8-byte word of the table (a
+      // segment's groups start at a multiple of 4): a wave-uniform scalar
       // load (lgkmcnt), never a VMEM load the compiler would wait for with
       // vmcnt(0) behind the ring's DMAs.
-      const int gi = __builtin_amdgcn_readfirstlane(grp0 + 2 * ch);
-      const uint32_t gw = reinterpret_cast<const uint32_t*>(a.grp)[gi >> 1];
-      int g0 = (int16_t)(gw & 0xffffu), g1 = (int16_t)(gw >> 16);
-      g0 = g0 < 0 ? g_safe : g0;
-      g1 = g1 < 0 ? g_safe : g1;
+      const int gi = __builtin_amdgcn_readfirstlane(grp0 + 4 * ch);
+      const uint2 gw = reinterpret_cast<const uint2*>(a.grp)[gi >> 2];
+      int gq[4] = {(int16_t)(gw.x & 0xffffu), (int16_t)(gw.x >> 16),
+                   (int16_t)(gw.y & 0xffffu), (int16_t)(gw.y >> 16)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gq[e] = gq[e] < 0 ? g_safe : gq[e];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int g = (bc[i] >> 1) ? g1 : g0;
-        dma16_sb(Bp, boff[i] + (uint32_t)g * 32u, lds_addr(X + 1024 + 64 * (4 * wave + i)));
+        const int g = bc[i] == 0 ? gq[0] : bc[i] == 1 ? gq[1] : bc[i] == 2 ? gq[2] : gq[3];
+        dma16_sb(Bp, boff[i] + (uint32_t)g * 16u, lds_addr(X + 1024 + 64 * (4 * wave + i)));
       }
     };
     uint4 ta[2], tb[8];
@@ -693,11 +694,11 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
     m = m < mlast ? m : mlast;
     xoff[i] = (uint32_t)(((long long)m * a.ldx + 8 * c) * 2);
   }
-  // A rows: stacked column col -> row 16 * (g & 4095) + col % 16 of stack
-  // A[g >> 12], g = grp[col / 16]; padding groups (and columns past n_cols)
+  // A rows: stacked column col -> row 8 * (g & 4095) + col % 8 of stack
+  // A[g >> 12], g = grp[col / 8]; padding groups (and columns past n_cols)
   // read the first live group's rows (finite; their T columns are exactly 0
-  // or never written). One DMA instruction covers 8 columns of one 16-group,
-  // so its stack (its scalar base) is uniform across the wave.
+  // or never written). One DMA instruction covers the 8 columns of one
+  // group, so its stack (its scalar base) is uniform across the wave.
   const int g_safe = a.grp[0];
   uint32_t aoff[4];
   int asrc[4];
@@ -707,9 +708,9 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
     const int r = p >> 3;
     const int c = (p & 7) ^ ((r >> 1) & 7);
     const int col = c0 + r;
-    const int g = col < a.n_cols ? a.grp[col >> 4] : -1;
+    const int g = col < a.n_cols ? a.grp[col >> 3] : -1;
     const int gs = g < 0 ? g_safe : g;
-    const int row = 16 * (gs & 4095) + (g < 0 ? 0 : (col & 15));
+    const int row = 8 * (gs & 4095) + (g < 0 ? 0 : (col & 7));
     aoff[i] = (uint32_t)(((long long)row * a.K + 8 * c) * 2);
     asrc[i] = __builtin_amdgcn_readfirstlane(gs >> 12);
   }
@@ -809,7 +810,7 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
       for (int q = 0; q < 4; ++q) {
         const int c = c0 + 64 * wc + 32 * j + 8 * q + 4 * fk;
         if (kslices == 1) {
-          const float f = a.coef[c >> 4];
+          const float f = a.coef[c >> 3];
           uint2 v;
           if (f == 0.0f) {
             v = make_uint2(0, 0);
@@ -844,7 +845,7 @@ __global__ void lora_xa_reduce_kernel(const float* part, int kslices, int M,
           part + ((long long)k * M + m) * n_cols + c);
       s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
-    const float f = a.coef[c >> 4];
+    const float f = a.coef[c >> 3];
     uint2 o;
     if (f == 0.0f) {
       o = make_uint2(0, 0);

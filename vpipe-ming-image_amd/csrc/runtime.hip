@@ -138,10 +138,10 @@ hipError_t profiled(ming_ctx* c, int bucket, double flops, double bytes,
 
 struct LoraBind {
   int rank = 0;     // as bound
-  int rank16 = 0;   // padded to 16 (zero rows / columns)
+  int rank8 = 0;    // padded to 8 (zero rows / columns)
   float fold = 1.0f;
-  uint16_t* A = nullptr;  // [rank16][K]
-  uint16_t* B = nullptr;  // [N_seg][rank16]
+  uint16_t* A = nullptr;  // [rank8][K]
+  uint16_t* B = nullptr;  // [N_seg][rank8]
 };
 
 struct Segment {
@@ -165,15 +165,15 @@ struct ming_qweight {
   uint16_t* w16 = nullptr;
   std::vector<Segment> segs;
   // Stacked adapter factors, rebuilt when a binding changes:
-  //   A_all [R16_all][K]     every (segment, slot) in order
-  //   B_seg[s] [N_s][R16_s]  per segment, its slots in order
+  //   A_all [R8_all][K]     every (segment, slot) in order
+  //   B_seg[s] [N_s][R8_s]  per segment, its slots in order
   bool stacks_dirty = true;
   uint16_t* A_all = nullptr;
   std::vector<uint16_t*> B_seg;
   std::vector<int> a_row0;   // [seg*8 + slot] row in A_all
   int a_rows = 0;            // rows of A_all
   std::vector<int> b_col0;   // [seg*8 + slot] column in B_seg[seg]
-  std::vector<int> b_ld;     // per segment: R16 of the segment
+  std::vector<int> b_ld;     // per segment: R8 of the segment
   // bumped by every bind and unbind: a model's caption cache keys on the
   // context-refiner weights' generations, so a direct rebinding of one of
   // them is never served stale rows
@@ -210,8 +210,8 @@ int build_stacks(ming_qweight* q) {
       if (b.rank <= 0) continue;
       q->a_row0[si * MING_MAX_LORA_SLOTS + sl] = rows_all;
       q->b_col0[si * MING_MAX_LORA_SLOTS + sl] = col;
-      rows_all += b.rank16;
-      col += b.rank16;
+      rows_all += b.rank8;
+      col += b.rank8;
     }
     q->b_ld[si] = col;
   }
@@ -233,12 +233,12 @@ int build_stacks(ming_qweight* q) {
       const int ar = q->a_row0[si * MING_MAX_LORA_SLOTS + sl];
       const int bc = q->b_col0[si * MING_MAX_LORA_SLOTS + sl];
       MING_HIP(hipMemcpyAsync(q->A_all + (size_t)ar * K, b.A,
-                              (size_t)b.rank16 * K * 2,
+                              (size_t)b.rank8 * K * 2,
                               hipMemcpyDeviceToDevice, s),
                "A stack copy");
       MING_HIP(hipMemcpy2DAsync(q->B_seg[si] + bc, (size_t)q->b_ld[si] * 2,
-                                b.B, (size_t)b.rank16 * 2,
-                                (size_t)b.rank16 * 2, (size_t)sg.N,
+                                b.B, (size_t)b.rank8 * 2,
+                                (size_t)b.rank8 * 2, (size_t)sg.N,
                                 hipMemcpyDeviceToDevice, s),
                "B stack copy");
     }
@@ -704,13 +704,13 @@ int ming_qweight_concat(ming_ctx* c, int n_parts, ming_qweight* const* parts,
       const LoraBind& b = p->segs[0].slot[sl];
       if (b.rank <= 0) continue;
       LoraBind& d = sg.slot[sl];
-      d.rank = b.rank; d.rank16 = b.rank16; d.fold = b.fold;
-      chk(hipMalloc(&d.A, (size_t)b.rank16 * K * 2), "concat lora alloc");
-      chk(hipMalloc(&d.B, (size_t)p->N * b.rank16 * 2), "concat lora alloc");
+      d.rank = b.rank; d.rank8 = b.rank8; d.fold = b.fold;
+      chk(hipMalloc(&d.A, (size_t)b.rank8 * K * 2), "concat lora alloc");
+      chk(hipMalloc(&d.B, (size_t)p->N * b.rank8 * 2), "concat lora alloc");
       if (rc != MING_OK) break;
-      chk(hipMemcpyAsync(d.A, b.A, (size_t)b.rank16 * K * 2,
+      chk(hipMemcpyAsync(d.A, b.A, (size_t)b.rank8 * K * 2,
                          hipMemcpyDeviceToDevice, s), "concat lora copy");
-      chk(hipMemcpyAsync(d.B, b.B, (size_t)p->N * b.rank16 * 2,
+      chk(hipMemcpyAsync(d.B, b.B, (size_t)p->N * b.rank8 * 2,
                          hipMemcpyDeviceToDevice, s), "concat lora copy");
     }
     nb += p->N;
@@ -752,24 +752,24 @@ int ming_qweight_bind_lora(ming_qweight* q, int segment, int slot, int rank,
   ming_ctx* c = q->ctx;
   DeviceGuard g(c->device);
   Segment& sg = q->segs[segment];
-  const int r16 = round_up(rank, 16);
+  const int r8 = round_up(rank, 8);
   const size_t K = (size_t)q->K;
   LoraBind nb;
-  nb.rank = rank; nb.rank16 = r16; nb.fold = fold;
-  if (hipMalloc(&nb.A, (size_t)r16 * K * 2) != hipSuccess ||
-      hipMalloc(&nb.B, (size_t)sg.N * r16 * 2) != hipSuccess) {
+  nb.rank = rank; nb.rank8 = r8; nb.fold = fold;
+  if (hipMalloc(&nb.A, (size_t)r8 * K * 2) != hipSuccess ||
+      hipMalloc(&nb.B, (size_t)sg.N * r8 * 2) != hipSuccess) {
     if (nb.A) (void)hipFree(nb.A);
     if (nb.B) (void)hipFree(nb.B);
     return fail(MING_ERR_ALLOC, "bind_lora: allocation failed");
   }
   const hipMemcpyKind kind =
       src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-  hipError_t e = hipMemsetAsync(nb.A, 0, (size_t)r16 * K * 2, c->stream);
-  if (e == hipSuccess) e = hipMemsetAsync(nb.B, 0, (size_t)sg.N * r16 * 2, c->stream);
+  hipError_t e = hipMemsetAsync(nb.A, 0, (size_t)r8 * K * 2, c->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(nb.B, 0, (size_t)sg.N * r8 * 2, c->stream);
   if (e == hipSuccess)
     e = hipMemcpyAsync(nb.A, A, (size_t)rank * K * 2, kind, c->stream);
   if (e == hipSuccess)
-    e = hipMemcpy2DAsync(nb.B, (size_t)r16 * 2, B, (size_t)rank * 2,
+    e = hipMemcpy2DAsync(nb.B, (size_t)r8 * 2, B, (size_t)rank * 2,
                          (size_t)rank * 2, (size_t)sg.N, kind, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) {
@@ -825,7 +825,7 @@ struct LinOut {
 // n projections over the same x [M][K] (q, k, v; w1, w3): x is converted to
 // fp16 once for all of them (`xh_src`, when set, is that copy already made,
 // row stride K), and every live adapter of every one of them goes into ONE
-// stacked x.A launch -- the stacks' 16-rank groups side by side in T, group
+// stacked x.A launch -- the stacks' 8-rank groups side by side in T, group
 // entries naming their weight -- before each projection's GEMM reads its own
 // columns of T. n == 1 is lin() (ming-dit.cc:1763-1771).
 // Where one call's scratch comes from: the context's buffers, grown on
@@ -912,7 +912,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
   // The live stacks, per weight and segment, in slot order.
   ming::QprojArgs qa[ming::kMaxXaSources] = {};
   ming::LoraXaArgs xa{};
-  int xa_groups = 0;   // 16-wide groups of T over every weight and segment
+  int xa_groups = 0;   // 8-wide groups of T over every weight and segment
   uint64_t lora_flops[ming::kMaxXaSources] = {};
   int live_segs[ming::kMaxXaSources] = {};
   double xa_flops = 0.0, tail_flops[ming::kMaxXaSources] = {};
@@ -940,7 +940,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       ming::QprojSeg& d = qa[i].seg[si];
       d.n_begin = sg.n_begin;
       d.n_end = sg.n_begin + sg.N;
-      d.t_col0 = xa_groups * 16;
+      d.t_col0 = xa_groups * 8;
       d.grp0 = qp_groups;
       d.chunks = 0;
       d.ldb = any_live ? q->b_ld[si] : 0;
@@ -951,13 +951,13 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
         if (b.rank <= 0 || !scales || scales[sl] == 0.0f) continue;
         const int ar = q->a_row0[si * MING_MAX_LORA_SLOTS + sl];
         const int bc = q->b_col0[si * MING_MAX_LORA_SLOTS + sl];
-        for (int gi = 0; gi < b.rank16 / 16; ++gi) {
+        for (int gi = 0; gi < b.rank8 / 8; ++gi) {
           if (xa_groups + seg_groups >= ming::kMaxGroups ||
               qp_groups + seg_groups >= ming::kMaxGroups)
             return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
-          xa.grp[xa_groups + seg_groups] = (int16_t)((i << 12) | (ar / 16 + gi));
+          xa.grp[xa_groups + seg_groups] = (int16_t)((i << 12) | (ar / 8 + gi));
           xa.coef[xa_groups + seg_groups] = b.fold * scales[sl];
-          qa[i].grp[qp_groups + seg_groups] = (int16_t)(bc / 16 + gi);
+          qa[i].grp[qp_groups + seg_groups] = (int16_t)(bc / 8 + gi);
           ++seg_groups;
         }
         lora_flops[i] += 2ull * (uint64_t)M * (uint64_t)b.rank * (uint64_t)(q->K + sg.N);
@@ -967,7 +967,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       if (seg_groups == 0) continue;
       ++live_segs[i];
       // pad the segment's T columns to whole 32-rank chunks with zero groups
-      const int padded = round_up(seg_groups, 2);
+      const int padded = round_up(seg_groups, 4);
       for (int gi = seg_groups; gi < padded; ++gi) {
         if (xa_groups + gi >= ming::kMaxGroups || qp_groups + gi >= ming::kMaxGroups)
           return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
@@ -975,21 +975,21 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
         xa.coef[xa_groups + gi] = 0.0f;
         qa[i].grp[qp_groups + gi] = -1;
       }
-      d.chunks = padded / 2;
+      d.chunks = padded / 4;
       xa_groups += padded;
       qp_groups += padded;
     }
   }
   // the x.A kernels write T in 64-column blocks: zero groups after the last
   // segment make the stack a whole number of them
-  while (xa_groups % 4 != 0) {
+  while (xa_groups % 8 != 0) {
     if (xa_groups >= ming::kMaxGroups)
       return fail(MING_ERR_SHAPE, "ming_lin: live adapter ranks exceed 4096");
     xa.grp[xa_groups] = -1;
     xa.coef[xa_groups] = 0.0f;
     ++xa_groups;
   }
-  const int t_cols = xa_groups * 16;
+  const int t_cols = xa_groups * 8;
   // the fast x.A addresses x and each A stack as 64-bit bases plus 32-bit
   // byte offsets; its K split (slices summed in f32 by a second launch)
   const bool xa_fast = t_cols > 0 && c->route != MING_ROUTE_GENERAL && ldx % 8 == 0 &&
@@ -1036,7 +1036,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     }
     const bool dense_sk =
         q->bits == 16 && c->route != MING_ROUTE_GENERAL && live_segs[i] == 0 && !o.gate &&
-        !o.yh && tiles < 64 && q->N % 64 == 0 && q->N <= 16 * ming::kMaxGroups &&
+        !o.yh && tiles < 64 && q->N % 64 == 0 && q->N <= 8 * ming::kMaxGroups &&
         K % 64 == 0 && o.ldy <= (1 << 30) && (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) &&
         (uint64_t)q->N * (uint64_t)K * 2 <= (1ull << 32);
     if (dense_sk) {
@@ -1135,7 +1135,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       ming::LoraXaArgs da{};
       da.x = x; da.ldx = ldx; da.A[0] = q->w16; da.K = K; da.M = M;
       da.n_cols = q->N; da.t = o.y; da.ldt = (int)o.ldy;
-      for (int gi = 0; gi < q->N / 16; ++gi) {
+      for (int gi = 0; gi < q->N / 8; ++gi) {
         da.grp[gi] = (int16_t)gi;
         da.coef[gi] = 1.0f;
       }
