@@ -973,12 +973,13 @@ hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s) {
 //    one projection's 2.5 and q|k|v's 7.5 at the config-2 adapter set. At
 //    4352 rows that is 3 slices, measured best of 1, 2, 3, 5 and 8 over the
 //    1024^2 forward's 136 launches (6.59 ms against 6.91 ms for 5).
-//  - K > 4096 (the FFN-width input of w2, whose x.A always runs alone): 3
-//    blocks, i.e. 5 slices at 4352 rows, one round of 255 blocks (forward
-//    65.18 ms against 65.57 ms for 3 slices and 65.57 ms for 8).
+//  - K > 4096 (the FFN-width input of w2, whose x.A always runs alone): 2
+//    blocks (the config-2 set's 256 packed ranks), i.e. 7 slices at 4352
+//    rows, one round of 238 blocks: w2's x.A 3.7 us faster than with 5
+//    slices (3 blocks, 255 blocks of 32 K steps each).
 int lora_xa_fast_slices(int M, int n_cols, int K) {
   (void)n_cols;
-  const int tiles = ((M + 255) / 256) * (K > 4096 ? 3 : 5);
+  const int tiles = ((M + 255) / 256) * (K > 4096 ? 2 : 5);
   const int KT = K / 64;
   int ks = 256 / (tiles > 0 ? tiles : 1);       // about one round of the chip
   const int kmax = KT / 8 > 1 ? KT / 8 : 1;      // keep >= 8 K steps per slice
