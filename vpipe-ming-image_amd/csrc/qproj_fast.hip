@@ -638,31 +638,31 @@ __global__ void qproj_split_reduce_kernel(const QprojArgs a) {
 }
 
 // ---- T = x . A_live^T * coef: the adapters' stacked down-projection --------
-// Block tile 256 rows x 128 stacked ranks; 4 waves in 2 x 2, each 128 rows x
-// 64 ranks (4 x 2 tiles of v_mfma_f32_32x32x16_bf16, D[rank][row], so a lane
-// owns one row and 4 consecutive ranks per register quad). Split-K over
-// kslices so the grid is about one round of the chip; slice s writes f32
-// partials P[s] and lora_xa_reduce_kernel sums the slices in a fixed order
-// (no atomics: the bits do not depend on timing). With one slice the block
-// writes T directly. The stage ring is the projection kernel's: three
-// stages of [x 32 KB | A 16 KB] filled by inline-asm DMA, each wave's DMA
-// group of stage kt+2 issued one per k16 step, the wait + barrier between
-// steps 2 and 3, and step 3 reading the next stage's first fragments.
-__global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a,
-                                                              float* part,
+// Block tile 256 rows x 128 stacked ranks. Four MFMA waves in 2 x 2, each
+// 128 rows x 64 ranks (4 x 2 tiles of v_mfma_f32_32x32x16_bf16, D[rank][row],
+// so a lane owns one row and 4 consecutive ranks per register quad), and a
+// DMA-only wave beside each on its SIMD: a global_load_lds holds the wave
+// that issues it for ~16 cycles its MFMAs do not hide, so no MFMA wave
+// issues one. Split-K over kslices so the grid is about one round of the
+// chip; slice s writes f32 partials P[s] and lora_xa_reduce_kernel sums the
+// slices in a fixed order (no atomics: the bits do not depend on timing).
+// With one slice the block writes T directly. A three-stage ring of [x 32 KB
+// | A 16 KB] filled by inline-asm DMA, one barrier a stage, which every wave
+// passes once: before it the DMA waves issue stage t + 2 into the buffer
+// stage t - 1 left and wait until stage t + 1 has landed; the MFMA waves
+// have then finished every read of stage t (steps 0-2 read it; step 3,
+// after the barrier, reads stage t + 1's first fragments).
+__global__ __launch_bounds__(512, 1) void lora_xa_fast_kernel(const LoraXaArgs a, float* part,
                                                               int kslices) {
   constexpr int STG = 256 * 8 + 128 * 8;         // x tile + A tile, 16-B chunks
-  constexpr int PER = 12;                        // 8 x + 4 A DMAs per wave
+  constexpr int PER = 12;                        // 8 x + 4 A DMAs per DMA wave
   __shared__ uint4 st0[STG], st1[STG], st2[STG];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool dma_wave = wave >= 4;
+  const int rw = wave & 3;                       // the role's wave index
   const int fr = lane & 31, fk = lane >> 5;
-  const int wm = wave & 1, wc = wave >> 1;
-  // XCD-aware order: block b runs on XCD b % 8, so each XCD takes a
-  // contiguous run of work items, ordered (slice, row block, column block)
-  // with the column blocks fastest. The blocks that read the same x rows
-  // then run side by side on one XCD and share its L2 instead of each
-  // fetching x from HBM.
+  const int wm = rw & 1, wc = rw >> 1;
   int m0, c0, ks;
   {
     const int tiles_m = (a.M + 255) / 256, tiles_c = (a.n_cols + 127) / 128;
@@ -680,53 +680,63 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
   const int kt1 = (int)((long long)KT * (ks + 1) / kslices);
   const int NT = kt1 - kt0;
   const int mlast = a.M - 1;
-  // a wave whose 64 ranks lie past n_cols (n_cols % 128 == 64) skips its
-  // MFMAs; it still issues and waits like the others
-  const bool live = c0 + 64 * wc < a.n_cols;
 
-  uint32_t xoff[8];
+  if (dma_wave) {
+    uint32_t xoff[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int p = 64 * (8 * wave + i) + lane;
-    const int row = p >> 3;
-    const int c = (p & 7) ^ ((row >> 1) & 7);
-    int m = m0 + row;
-    m = m < mlast ? m : mlast;
-    xoff[i] = (uint32_t)(((long long)m * a.ldx + 8 * c) * 2);
-  }
-  // A rows: stacked column col -> row 8 * (g & 4095) + col % 8 of stack
-  // A[g >> 12], g = grp[col / 8]; padding groups (and columns past n_cols)
-  // read the first live group's rows (finite; their T columns are exactly 0
-  // or never written). One DMA instruction covers the 8 columns of one
-  // group, so its stack (its scalar base) is uniform across the wave.
-  const int g_safe = a.grp[0];
-  uint32_t aoff[4];
-  int asrc[4];
+    for (int i = 0; i < 8; ++i) {
+      const int p = 64 * (8 * rw + i) + lane;
+      const int row = p >> 3;
+      const int c = (p & 7) ^ ((row >> 1) & 7);
+      int m = m0 + row;
+      m = m < mlast ? m : mlast;
+      xoff[i] = (uint32_t)(((long long)m * a.ldx + 8 * c) * 2);
+    }
+    const int g_safe = a.grp[0];
+    uint32_t aoff[4];
+    int asrc[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p = 64 * (4 * wave + i) + lane;
-    const int r = p >> 3;
-    const int c = (p & 7) ^ ((r >> 1) & 7);
-    const int col = c0 + r;
-    const int g = col < a.n_cols ? a.grp[col >> 3] : -1;
-    const int gs = g < 0 ? g_safe : g;
-    const int row = 8 * (gs & 4095) + (g < 0 ? 0 : (col & 7));
-    aoff[i] = (uint32_t)(((long long)row * a.K + 8 * c) * 2);
-    asrc[i] = __builtin_amdgcn_readfirstlane(gs >> 12);
-  }
-  auto issue_grp = [&](int g, int kt, const uint4* S) {
-    if (g < 2) {
+    for (int i = 0; i < 4; ++i) {
+      const int p = 64 * (4 * rw + i) + lane;
+      const int r = p >> 3;
+      const int c = (p & 7) ^ ((r >> 1) & 7);
+      const int col = c0 + r;
+      const int g = col < a.n_cols ? a.grp[col >> 3] : -1;
+      const int gs = g < 0 ? g_safe : g;
+      const int row = 8 * (gs & 4095) + (g < 0 ? 0 : (col & 7));
+      aoff[i] = (uint32_t)(((long long)row * a.K + 8 * c) * 2);
+      asrc[i] = __builtin_amdgcn_readfirstlane(gs >> 12);
+    }
+    auto issue = [&](int kt, const uint4* S) {
       const void* base = a.x + (long long)kt * 64;
 #pragma unroll
-      for (int i = 4 * g; i < 4 * g + 4; ++i)
-        dma16_sb(base, xoff[i], lds_addr(S + 64 * (8 * wave + i)));
-    } else {
+      for (int i = 0; i < 8; ++i) dma16_sb(base, xoff[i], lds_addr(S + 64 * (8 * rw + i)));
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         dma16_sb(a.A[asrc[i]] + (long long)kt * 64, aoff[i],
-                 lds_addr(S + 2048 + 64 * (4 * wave + i)));
+                 lds_addr(S + 2048 + 64 * (4 * rw + i)));
+    };
+    issue(kt0, st0);
+    issue(kt0 + (NT > 1 ? 1 : 0), st1);
+    ring_wait<PER>();                             // stage 0 landed
+    // stage t: stage t + 2 (a re-read of the last past the end) into the
+    // buffer of stage t - 1, then stage t + 1 landed, then the barrier
+    auto step = [&](int t, const uint4* Pv) {
+      issue(kt0 + (t + 2 < NT ? t + 2 : NT - 1), Pv);
+      ring_wait<PER>();
+    };
+    int t = 0;
+    for (; t + 3 <= NT; t += 3) {
+      step(t, st2);
+      step(t + 1, st0);
+      step(t + 2, st1);
     }
-  };
+    if (NT - t >= 1) step(t, st2);
+    if (NT - t == 2) step(t + 1, st0);
+    // no DMA outlives the block; no barrier: the MFMA waves meet no more
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
 
   floatx16_t acc[4][2];
 #pragma unroll
@@ -735,8 +745,7 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  // fragments of one k16 step: x rows 128wm + 32i + fr, A rows 64wc + 32j + fr
+  const bool live = c0 + 64 * wc < a.n_cols;
   uint4 xb[4], ab[2];
   auto read_frags = [&](const uint4* S, int kk, uint4 (&xv)[4], uint4 (&av)[2]) {
     const int c = 2 * kk + fk;
@@ -745,17 +754,12 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
 #pragma unroll
     for (int j = 0; j < 2; ++j) av[j] = S[2048 + swz8(64 * wc + 32 * j + fr, c)];
   };
-  auto body = [&](int t, const uint4* C, const uint4* Nx, const uint4* Pv) {
-    const int nk = kt0 + (t + 2 < NT ? t + 2 : NT - 1);
+  auto body = [&](const uint4* C, const uint4* Nx) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       uint4 xn[4], an[2];
-      if (kk < 3) {
-        issue_grp(kk, nk, Pv);
-        read_frags(C, kk + 1, xn, an);
-      } else {
-        read_frags(Nx, 0, xn, an);
-      }
+      if (kk < 3) read_frags(C, kk + 1, xn, an);
+      else read_frags(Nx, 0, xn, an);
       if (live) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -772,7 +776,7 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
       }
       __builtin_amdgcn_sched_barrier(0);
       if (kk == 2) {
-        ring_wait<PER>();                        // stage t+1 landed, t done
+        ring_wait<0>();                          // (no DMAs of its own) reads done + barrier
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -781,22 +785,16 @@ __global__ __launch_bounds__(256, 1) void lora_xa_fast_kernel(const LoraXaArgs a
       for (int j = 0; j < 2; ++j) ab[j] = an[j];
     }
   };
-
-#pragma unroll
-  for (int g = 0; g < 3; ++g) issue_grp(g, kt0, st0);
-#pragma unroll
-  for (int g = 0; g < 3; ++g) issue_grp(g, kt0 + (NT > 1 ? 1 : 0), st1);
-  ring_wait<PER>();
+  ring_wait<0>();                                // stage 0 landed (the DMA waves' wait)
   read_frags(st0, 0, xb, ab);
   int t = 0;
   for (; t + 3 <= NT; t += 3) {
-    body(t, st0, st1, st2);
-    body(t + 1, st1, st2, st0);
-    body(t + 2, st2, st0, st1);
+    body(st0, st1);
+    body(st1, st2);
+    body(st2, st0);
   }
-  if (NT - t >= 1) body(t, st0, st1, st2);
-  if (NT - t == 2) body(t + 1, st1, st2, st0);
-  ring_wait<0>();                                // no DMA outlives the block
+  if (NT - t >= 1) body(st0, st1);
+  if (NT - t == 2) body(st1, st2);
 
   if (!live) return;
   // D[c][m]: lane owns row m, four consecutive ranks per register quad.
@@ -1002,7 +1000,7 @@ hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s) {
   if (a.M <= 0 || a.n_cols <= 0) return hipSuccess;
   const unsigned nblk = (unsigned)(((a.M + 255) / 256) * ((a.n_cols + 127) / 128) * kslices);
-  hipLaunchKernelGGL(lora_xa_fast_kernel, dim3(nblk), dim3(256), 0, s, a, part, kslices);
+  hipLaunchKernelGGL(lora_xa_fast_kernel, dim3(nblk), dim3(512), 0, s, a, part, kslices);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || kslices == 1) return e;
   long long work = (long long)a.M * (a.n_cols / 4);
