@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MING_ABI_VERSION 4
+#define MING_ABI_VERSION 5
 
 /* Runtime-LoRA slots: lora::Stack::kMax (ming-dit.h:117) and the eight
  * `lora`..`lora8` keys (ming-model-config-stage.h:37-56). */
@@ -70,6 +70,9 @@ typedef struct ming_engagement {
   int64_t gemm_split;     /* of the fast-route projections, those split along K (< 64 tiles) */
   int64_t range_faults;   /* synchronizations that found a saturated fp16 input copy
                              (MING_ERR_RANGE; see MING_ROUTE_WIDE) */
+  int64_t gemm_paired;    /* launches that ran a SwiGLU's gate and up projections together
+                             (ming_ffn on the fast route; each projection also counts in
+                             gemm_q4/q8 and gemm_fast) */
 } ming_engagement;
 
 /* Kernel routes for quantized projections. AUTO takes the fast route

@@ -18,7 +18,7 @@ def test_library_exports_every_header_symbol():
 
 
 def test_abi_version():
-    assert m.lib().ming_abi_version() == 4
+    assert m.lib().ming_abi_version() == 5
 
 
 def test_engagement_layout_matches_the_header():

@@ -346,26 +346,46 @@ def test_lin_swiglu_equals_lin_then_swiglu(ctx, orc, inplace):
     assert np.array_equal(from_dev(out), from_dev(ref))
 
 
-def test_ffn_equals_the_four_calls(ctx, orc):
-    """ming_ffn == lin(w1), lin(w3), swiglu, lin(w2) bit for bit, with the
-    config-2 adapter set live on all three projections."""
-    M, H, F = 260, 384, 640
-    w1, w3, w2 = _ffn_weights(ctx, 620, H, F)
-    x = to_dev(bf16(randn(621, (M, H))))
-    g = to_dev(_run(ctx, w1, x, M, CFG2_SCALES))
-    u = to_dev(_run(ctx, w3, x, M, CFG2_SCALES))
+def _ffn_four_calls(ctx, w1, w3, w2, x, M, F, scales):
+    g = to_dev(_run(ctx, w1, x, M, scales))
+    u = to_dev(_run(ctx, w3, x, M, scales))
     a = empty_bf16(M, F)
     sync()
     ctx.swiglu(g, u, a, M, F)
     sync()
-    ref = _run(ctx, w2, a, M, CFG2_SCALES)
+    return from_dev(a), _run(ctx, w2, a, M, scales)
+
+
+@pytest.mark.parametrize("M,H,F,bits,w3_slots,scales", [
+    (260, 384, 640, 4, 8, CFG2_SCALES),     # the config-2 set on all three
+    (300, 256, 320, 8, 8, CFG2_SCALES),     # w8, F not a whole 128-column tile
+    (513, 256, 448, 4, 8, None),            # no live adapter: no tail at all
+    (260, 384, 640, 4, 6, CFG2_SCALES),     # w3 with fewer tail chunks than w1
+])
+def test_ffn_equals_the_four_calls(ctx, orc, M, H, F, bits, w3_slots, scales):
+    """ming_ffn == lin(w1), lin(w3), swiglu, lin(w2) bit for bit, h included.
+    On the fast route w1 and w3 run as one paired launch (128 columns of each
+    per tile, the SwiGLU taken in LDS) unless their LoRA tails differ in
+    length; either way the bits are the separate calls'."""
+    print(f"case ffn M={M} H={H} F={F} bits={bits} w3_slots={w3_slots}", flush=True)
+    w1, w3, w2 = _ffn_weights(ctx, 620, H, F, bits)
+    for s in range(w3_slots, 8):
+        w3.unbind_lora(s)
+    x = to_dev(bf16(randn(621, (M, H))))
+    h_ref, ref = _ffn_four_calls(ctx, w1, w3, w2, x, M, F, scales)
     y = empty_bf16(M, H)
+    sync()
     e0 = ctx.engagement()
-    ctx.ffn(w1, w3, w2, x, y, M, CFG2_SCALES)
+    h = ctx.ffn(w1, w3, w2, x, y, M, scales)
     sync()
     e1 = ctx.engagement()
-    assert e1["gemm_q4"] - e0["gemm_q4"] == 3
-    assert e1["lora_proj"] - e0["lora_proj"] == 3
+    assert e1["gemm_q4" if bits == 4 else "gemm_q8"] - e0["gemm_q4" if bits == 4 else "gemm_q8"] == 3
+    assert e1["lora_proj"] - e0["lora_proj"] == (3 if scales else 0)
+    # the config-2 set ends in its rank-128 slot 7, so unbinding slots 6-7
+    # leaves w3 fewer 32-rank chunks than w1
+    paired = route_is_auto(ctx) and w3_slots == 8
+    assert e1["gemm_paired"] - e0["gemm_paired"] == (1 if paired else 0)
+    assert np.array_equal(from_dev(h), h_ref)
     assert np.array_equal(from_dev(y), ref)
 
 
@@ -549,8 +569,10 @@ def test_config2_ffn_full_size(ctx, orc):
     3840 -> 10240 and w2 10240 -> 3840 as w4g64 packs of N(0, 0.02) weights,
     the eight slots {4, 8, 16, 16, 32, 32, 64, 128} at strengths
     {1, .5, 0, -.3, .8, 0, 1.2, .25} on all three, through ming_ffn (the
-    bench's step). 17 x 40 = 680 tiles: the unsplit w4 kernel with the
-    8-chunk tail and, on w3, the fused SwiGLU epilogue. On a row sample over
+    bench's step). On the fast route w1 and w3 run as one paired launch
+    (17 x 80 tiles of 128 columns of each, the SwiGLU taken in LDS) and w2 as
+    the unsplit w4 kernel (17 x 15 tiles), each with the 8-chunk tail. On a
+    row sample over
     all 17 M tiles, against the oracle (gpu_ff, ming-dit.cc:2151-2162):
       h (w3's fused epilogue) vs swiglu(bf16(x.W1'), bf16(x.W3')) and y vs
       the f32 reference of w2 on the kernel's own h: each stage on its own
@@ -589,6 +611,7 @@ def test_config2_ffn_full_size(ctx, orc):
     auto = route_is_auto(ctx)
     assert eng["gemm_q4"] == 3 and eng["lora_proj"] == 3 and eng["lora_xa"] == 2
     assert eng["gemm_fast"] == (3 if auto else 0) and eng["gemm_split"] == 0
+    assert eng["gemm_paired"] == (1 if auto else 0)
     rows = _cfg2_rows(M)
     assert len(rows) == 51 and rows[-1] == M - 1
     yh, hh = from_dev(y)[rows], from_dev(h)[rows]

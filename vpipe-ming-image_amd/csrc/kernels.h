@@ -65,6 +65,13 @@ struct QprojArgs {
   // kernel's x tiles, the fast epilogue's yh) met a bf16 value of magnitude
   // >= 2^16, inf or NaN (see range_report)
   int* range;
+  // The paired gated launch (launch_qproj_pair): the weight above is the
+  // gate projection (one segment, seg[0]) and (codes_u, sb_u, seg_u) the up
+  // projection of the same shape, its groups in grp[] from seg_u.grp0, its
+  // T columns in the same t; y = bf16(silu(bf16(gate)) * bf16(up)).
+  const uint32_t* codes_u;
+  const uint32_t* sb_u;
+  QprojSeg seg_u;
 };
 
 // wide: bits 4/8 run with bf16 activations and the weight as a bf16 pair
@@ -243,6 +250,13 @@ hipError_t validate_gemv_kernels();
 // ---- the fast quantized route (qproj_fast.hip) --------------------------------
 // x is fp16 (carrying bf16 values), a.codes / a.sb the fast resident layout.
 hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s);
+// The gate and up projections of a SwiGLU in one launch (the fields after
+// `range` in QprojArgs): each 256 x 256 tile holds 128 columns of each, so
+// the gate's output meets the up projection's in LDS and only
+// y = bf16(silu(gate) * up) (and its fp16 copy yh) is written. Both weights
+// one segment each with the same number of LoRA tail chunks, N % 8 == 0,
+// y 16-byte aligned with ldy % 8 == 0; no K split.
+hipError_t launch_qproj_pair(int bits, const QprojArgs& a, hipStream_t s);
 hipError_t launch_repack_fast(int bits, const uint32_t* codes,
                               const uint16_t* scales, const uint16_t* biases,
                               int N, int K, uint32_t* codes_f, uint32_t* sbf,

@@ -155,14 +155,23 @@ __device__ __forceinline__ int wchunk(int n, int h) {
 // b / tiles of tile b % tiles. The slice runs its share of K (the last one
 // also the LoRA tail) and writes f32 partials to a.part; the split reduce
 // then sums the slices in order and finishes as the epilogue does.
-template <int BITS, bool SPLIT>
-__global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
+//
+// PAIR (launch_qproj_pair): the tile's 256 weight rows are 128 rows of the
+// gate weight (waves 0-1) and the same 128 rows of the up weight (waves
+// 2-3); the tail stages the gate's and the up projection's T chunks side by
+// side; the epilogue meets the two in LDS and writes only the SwiGLU.
+template <int BITS, bool SPLIT, bool PAIR>
+__device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
   constexpr int WCH = BITS == 4 ? 512 : 1024;    // 16-B code chunks per stage
   constexpr int CPR = BITS == 4 ? 2 : 4;         // code chunks per row
   constexpr int WDMA = WCH / 256;                // code DMAs per wave per stage
   constexpr int PER = 8 + WDMA + 1;              // DMAs per wave per base stage
-  // One __shared__ object per stage: [x 32 KB | codes | (s, b)].
-  constexpr int STG = BM * 8 + WCH + BN / 4;
+  constexpr int TPER = PAIR ? 12 : 8;            // DMAs per wave per tail chunk
+  constexpr int BNT = PAIR ? BN / 2 : BN;        // output columns per tile
+  // One __shared__ object per stage: [x 32 KB | codes | (s, b)]; a tail
+  // chunk is [T 16 KB | B 16 KB (| the up projection's T 16 KB)].
+  constexpr int STG0 = BM * 8 + WCH + BN / 4;
+  constexpr int STG = PAIR && STG0 < 3072 ? 3072 : STG0;
   __shared__ uint4 st0[STG], st1[STG], st2[STG];
 
   // Waves split N only: wave w owns output columns [64w, 64w+64) for all
@@ -172,9 +181,12 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fk = lane >> 5;
+  // PAIR: waves 2-3 read the up weight; their columns are the gate's again
+  const bool upw = PAIR && wave >= 2;
+  const int wcol = PAIR ? 64 * (wave & 1) : 64 * wave;
 
   const int tiles_m = (a.M + BM - 1) / BM;
-  const int tiles_n = (a.N + BN - 1) / BN;
+  const int tiles_n = (a.N + BNT - 1) / BNT;
   int tm, tn, blk = (int)blockIdx.x, ks = 0, kt0 = 0;
   int KT = a.K / BK;
   if constexpr (SPLIT) {
@@ -184,14 +196,14 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     KT = KT * (ks + 1) / a.kslices - kt0;
   }
   tile_of_block(blk, tiles_m, tiles_n, &tm, &tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BM, n0 = tn * BNT;
   const int mlast = a.M - 1, nlast = a.N - 1;
 
   // stage 0 of this block's K range
   const _Float16* __restrict__ x16 = reinterpret_cast<const _Float16*>(a.x) + (long long)kt0 * BK;
   const uint4* __restrict__ codes =
-      reinterpret_cast<const uint4*>(a.codes) + (long long)kt0 * a.N * CPR;
-  const uint32_t* __restrict__ sbp = a.sb + (long long)kt0 * a.N;
+      reinterpret_cast<const uint4*>(upw ? a.codes_u : a.codes) + (long long)kt0 * a.N * CPR;
+  const uint32_t* __restrict__ sbp = (upw ? a.sb_u : a.sb) + (long long)kt0 * a.N;
 
   // DMA sources for this lane, per stage (advance by k).
   // x tile: wave issues chunks q = 8*wave + i; lane p = 64q + lane.
@@ -214,11 +226,11 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     const int p = 64 * (WDMA * wave + i) + lane;
     const int r = p / CPR;
     const int h = (p % CPR) ^ wswz<CPR>(r);
-    int n = n0 + r;
+    int n = n0 + (PAIR ? (r & 127) : r);
     n = n < nlast ? n : nlast;
     woff[i] = (uint32_t)((n * CPR + h) * 16);
   }
-  int sn = n0 + 64 * wave + lane;
+  int sn = n0 + wcol + lane;
   sn = sn < nlast ? sn : nlast;
   const uint32_t soff = (uint32_t)sn * 4u;
 
@@ -398,11 +410,15 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     if (n0 >= a.seg[i].n_begin) sg = i;
   const int chunks32 = (!SPLIT || ks == a.kslices - 1) ? a.seg[sg].chunks : 0;
   if (chunks32 > 0) {
+    // PAIR: waves 2-3 gather the up projection's B (its segment, its
+    // groups); both T chunks are staged for every wave
+    const QprojSeg& sw = upw ? a.seg_u : a.seg[sg];
     const int t_col0 = a.seg[sg].t_col0;
-    const int ldb = a.seg[sg].ldb;
-    const int grp0 = a.seg[sg].grp0;
-    const int seg_nb = a.seg[sg].n_begin, seg_ne = a.seg[sg].n_end;
-    const uint16_t* __restrict__ Bp = a.seg[sg].B;
+    const int ldb = sw.ldb;
+    const int grp0 = sw.grp0;
+    const int seg_nb = sw.n_begin, seg_ne = sw.n_end;
+    const uint16_t* __restrict__ Bp = sw.B;
+    const uint16_t* const tu = a.t + (PAIR ? a.seg_u.t_col0 - t_col0 : 0);
     // the first live group of the segment: a finite source for padding
     // groups (their T columns are exactly 0)
     const int g_safe = a.grp[grp0];
@@ -417,7 +433,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
       int m = m0 + row;
       m = m < mlast ? m : mlast;
       toff[i] = (uint32_t)(((long long)m * a.ldt + t_col0 + 8 * c) * 2);
-      int n = n0 + row;
+      int n = n0 + (PAIR ? (row & 127) : row);
       n = n < seg_ne - 1 ? n : seg_ne - 1;
       boff[i] = (uint32_t)((long long)(n - seg_nb) * ldb * 2);
       bc[i] = c;
@@ -429,6 +445,11 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         dma16_sb(a.t + 32 * ch, toff[i], lds_addr(X + 64 * (4 * wave + i)));
+      if constexpr (PAIR) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dma16_sb(tu + 32 * ch, toff[i], lds_addr(X + 2048 + 64 * (4 * wave + i)));
+      }
       // The chunk's four groups are one aligned 8-byte word of the table (a
       // segment's groups start at a multiple of 4): a wave-uniform scalar
       // load (lgkmcnt), never a VMEM load the compiler would wait for with
@@ -450,8 +471,9 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
       const int c = 2 * kk + fk;
 #pragma unroll
       for (int j = 0; j < 2; ++j) av[j] = X[1024 + swz4(64 * wave + 32 * j + fr, c)];
+      const uint4* const XT = upw ? X + 2048 : X;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) bv[i] = X[swz4(32 * i + fr, c)];
+      for (int i = 0; i < 8; ++i) bv[i] = XT[swz4(32 * i + fr, c)];
     };
     // Chunk ch: step 0 reads step 1's fragments and issues chunk ch+2 into
     // Pv; the wait + barrier sit between the steps; step 1 reads the next
@@ -481,7 +503,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
         if (kk == 0) {
-          ring_wait<8>();                       // chunk ch+1 landed, ch done
+          ring_wait<TPER>();                       // chunk ch+1 landed, ch done
           __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -492,7 +514,7 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     };
     issue_t(0, st0);
     issue_t(chunks32 > 1 ? 1 : 0, st1);
-    ring_wait<8>();
+    ring_wait<TPER>();
     read_t(st0, 0, ta, tb);
     int ch = 0;
     for (; ch + 3 <= chunks32; ch += 3) {
@@ -522,6 +544,69 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
                             acc[j][i][4 * q + 3]);
         }
     }
+    return;
+  }
+
+  if constexpr (PAIR) {
+    // The gate's and the up projection's bf16 outputs meet in LDS, 128 rows
+    // at a time: wave w writes its 64 columns to region w (as below), and
+    // after the barrier wave w reads column half c = w & 1 of rows
+    // [64 (w >> 1), +64) from the gate's region c and the up projection's
+    // region 2 + c, and writes y = bf16(silu(g) * u) and its fp16 copy: the
+    // bits of the gate's own epilogue followed by the gated one.
+    uint2* const Ew = reinterpret_cast<uint2*>((wave < 2 ? st0 : st1) + 1024 * (wave & 1));
+    const uint4* const Eg = st0 + 1024 * (wave & 1);
+    const uint4* const Eu = st1 + 1024 * (wave & 1);
+    const int cl = lane & 7;
+    const int n = n0 + wcol + 8 * cl;
+    uint32_t seen = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = 4 * h + ii;
+        const int ml = 32 * ii + fr;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int c = 4 * j + q;
+            uint2 v;
+            v.x = pack_bf16x2_rne(acc[j][i][4 * q + 0], acc[j][i][4 * q + 1]);
+            v.y = pack_bf16x2_rne(acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
+            Ew[ml * 16 + 2 * (c ^ ((ml >> 1) & 7)) + fk] = v;
+          }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int ml = 64 * (wave >> 1) + 8 * r + (lane >> 3);
+        const int e = ml * 8 + (cl ^ ((ml >> 1) & 7));
+        const uint4 gv = Eg[e];
+        uint4 v = Eu[e];
+        const int m = m0 + 128 * h + ml;
+        if (m < a.M && n < a.N) {
+          const uint32_t* gp = &gv.x;
+          uint32_t* vp = &v.x;
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2)
+            vp[e2] = pack_bf16x2_rne(silu_f(bf16_lo(gp[e2])) * bf16_lo(vp[e2]),
+                                     silu_f(bf16_hi(gp[e2])) * bf16_hi(vp[e2]));
+          *reinterpret_cast<uint4*>(a.y + (long long)m * a.ldy + n) = v;
+          if (a.yh) {
+            seen = range_track4(seen, v);
+            uint4 f;
+            f.x = bf16x2_to_f16x2(v.x);
+            f.y = bf16x2_to_f16x2(v.y);
+            f.z = bf16x2_to_f16x2(v.z);
+            f.w = bf16x2_to_f16x2(v.w);
+            *reinterpret_cast<uint4*>(a.yh + (long long)m * a.ldyh + n) = f;
+          }
+        }
+      }
+      __syncthreads();   // the next half rewrites the regions
+    }
+    if (a.yh) range_report(a.range, seen);
     return;
   }
 
@@ -601,6 +686,16 @@ __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
     }
   }
   if (a.yh) range_report(a.range, seen);
+}
+
+template <int BITS, bool SPLIT>
+__global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
+  qproj_fast_body<BITS, SPLIT, false>(a);
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256, 1) void qproj_pair_kernel(const QprojArgs a) {
+  qproj_fast_body<BITS, false, true>(a);
 }
 
 // The split projection's end: y = bf16(sum of the slices in order), then as
@@ -957,6 +1052,22 @@ hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((qproj_fast_kernel<4, false>), dim3(tiles), dim3(256), 0, s, a);
   else if (bits == 8)
     hipLaunchKernelGGL((qproj_fast_kernel<8, false>), dim3(tiles), dim3(256), 0, s, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_qproj_pair(int bits, const QprojArgs& a, hipStream_t s) {
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN / 2 - 1) / (BN / 2));
+  if (tiles <= 0) return hipSuccess;
+  if (a.kslices > 1 || a.g || !a.codes_u || !a.sb_u || a.nseg != 1 ||
+      a.seg[0].chunks != a.seg_u.chunks || a.N % 8 != 0 || a.ldy % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(a.y) & 15) != 0)
+    return hipErrorInvalidValue;
+  if (bits == 4)
+    hipLaunchKernelGGL((qproj_pair_kernel<4>), dim3(tiles), dim3(256), 0, s, a);
+  else if (bits == 8)
+    hipLaunchKernelGGL((qproj_pair_kernel<8>), dim3(tiles), dim3(256), 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

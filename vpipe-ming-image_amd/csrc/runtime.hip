@@ -915,6 +915,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
   int xa_groups = 0;   // 8-wide groups of T over every weight and segment
   uint64_t lora_flops[ming::kMaxXaSources] = {};
   int live_segs[ming::kMaxXaSources] = {};
+  int qp_used[ming::kMaxXaSources] = {};   // entries of qa[i].grp in use
   double xa_flops = 0.0, tail_flops[ming::kMaxXaSources] = {};
   bool xa_fits = true;
   for (int i = 0; i < n; ++i) {
@@ -979,6 +980,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       xa_groups += padded;
       qp_groups += padded;
     }
+    qp_used[i] = qp_groups;
   }
   // the x.A kernels write T in 64-column blocks: zero groups after the last
   // segment make the stack a whole number of them
@@ -1046,6 +1048,19 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     }
     if (o.gate && !fast[i]) up_bytes = std::max(up_bytes, (size_t)M * q->N * 2);
   }
+  // A SwiGLU's gate and up projections (the second gated by the first's
+  // output, as ming_ffn runs w1 and w3) on the fast route run as one launch:
+  // each tile computes 128 columns of both, and only the SwiGLU leaves the
+  // chip. Same bits as the two launches. It needs one segment per weight,
+  // the same number of LoRA tail chunks, no K split, and room for both
+  // group tables in one.
+  const bool pair = n == 2 && outs[1].gate && outs[1].gate == outs[0].y &&
+                    outs[1].ldg == outs[0].ldy && !outs[0].gate && !outs[0].yh && fast[0] &&
+                    fast[1] && split_ks[0] == 0 && split_ks[1] == 0 &&
+                    qs[0]->bits == qs[1]->bits && qs[0]->N == qs[1]->N && qs[0]->N % 8 == 0 &&
+                    qs[0]->segs.size() == 1 && qs[1]->segs.size() == 1 &&
+                    qa[0].seg[0].chunks == qa[1].seg[0].chunks &&
+                    qp_used[0] + qp_used[1] <= ming::kMaxGroups;
   // The fast route reads x as fp16 carrying the same (bf16) values: one
   // conversion serves every projection here.
   const bool need_xh = any_fast && !xh_src;
@@ -1102,6 +1117,40 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
                       [&] { return ming::launch_bf16_to_f16(x, ldx, dst, K, M, K,
                                                             c->stream, range_word(c)); }),
              "bf16->fp16 launch");
+  }
+  if (pair) {
+    const ming_qweight* q = qs[0];
+    const ming_qweight* u = qs[1];
+    const LinOut& o = outs[1];
+    ming::QprojArgs& a = qa[0];
+    a.x = xh; a.ldx = K; a.codes = q->codes_f; a.sb = q->sbf; a.w16 = nullptr;
+    a.y = o.y; a.ldy = o.ldy; a.M = M; a.N = q->N; a.K = K;
+    a.t = T; a.ldt = t_cols > 0 ? t_cols : 0; a.nseg = 1;
+    a.g = nullptr; a.ldg = 0;
+    a.yh = o.yh; a.ldyh = q->N;
+    a.range = range_word(c);
+    a.codes_u = u->codes_f; a.sb_u = u->sbf;
+    a.seg_u = qa[1].seg[0];
+    a.seg_u.grp0 += qp_used[0];
+    for (int gi = 0; gi < qp_used[1]; ++gi) a.grp[qp_used[0] + gi] = qa[1].grp[gi];
+    const double flops = 2.0 * 2.0 * M * (double)q->N * K + tail_flops[0] + tail_flops[1];
+    const double wbytes = 2.0 * ((double)q->N * K * q->bits / 8 + 4.0 * q->N * (K / 64));
+    MING_HIP(profiled(c, q->bits == 4 ? kBF4 : kBF8, flops,
+                      2.0 * M * K + wbytes + 2.0 * M * q->N,
+                      [&] { return ming::launch_qproj_pair(q->bits, a, c->stream); }),
+             "qproj pair launch");
+    for (int i = 0; i < 2; ++i) {
+      if (outs[i].took_fast) *outs[i].took_fast = true;
+      c->eng.gemm_fast += 1;
+      if (qs[i]->bits == 4) c->eng.gemm_q4 += 1;
+      else c->eng.gemm_q8 += 1;
+      c->eng.lora_proj += live_segs[i];
+      c->eng.gemm_flops +=
+          2ull * (uint64_t)M * (uint64_t)qs[i]->N * (uint64_t)K + lora_flops[i];
+    }
+    c->eng.elementwise += 1;
+    c->eng.gemm_paired += 1;
+    return ok();
   }
   for (int i = 0; i < n; ++i) {
     const ming_qweight* q = qs[i];

@@ -82,7 +82,8 @@ class Engagement(C.Structure):
                 ("attention", C.c_int64), ("elementwise", C.c_int64),
                 ("gemm_flops", C.c_uint64), ("gemm_fast", C.c_int64),
                 ("cap_cache_hits", C.c_int64), ("gemv", C.c_int64),
-                ("gemm_split", C.c_int64), ("range_faults", C.c_int64)]
+                ("gemm_split", C.c_int64), ("range_faults", C.c_int64),
+                ("gemm_paired", C.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
