@@ -98,13 +98,14 @@ namespace {
 // marks, ming-dit.cc:1689-1717, as HIP events around each launch).
 enum Bucket {
   kBQ4, kBQ8, kBDense, kBF4, kBF8, kBCvt, kBXa, kBRms, kBQkRope, kBRopeTab, kBSwiglu, kBResid,
-  kBModulate, kBBias, kBLn, kBQuant, kBAttn, kBNormRes, kBGemv, kBCount
+  kBModulate, kBBias, kBLn, kBQuant, kBAttn, kBNormRes, kBGemv, kBP4, kBP8, kBCount
 };
 const char* const kBucketName[kBCount] = {
     "qproj.w4", "qproj.w8", "qproj.dense", "qproj_fast.w4", "qproj_fast.w8",
     "cvt_f16", "lora_xa", "rmsnorm",
     "qk_norm_rope", "rope_table", "swiglu", "residual", "modulate",
-    "bias_act", "ln_modulate", "quantize", "attention", "norm_residual", "gemv"};
+    "bias_act", "ln_modulate", "quantize", "attention", "norm_residual", "gemv",
+    "qproj_pair.w4", "qproj_pair.w8"};
 
 hipEvent_t take_event(ming_ctx* c) {
   if (!c->pool.empty()) {
@@ -1135,7 +1136,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     for (int gi = 0; gi < qp_used[1]; ++gi) a.grp[qp_used[0] + gi] = qa[1].grp[gi];
     const double flops = 2.0 * 2.0 * M * (double)q->N * K + tail_flops[0] + tail_flops[1];
     const double wbytes = 2.0 * ((double)q->N * K * q->bits / 8 + 4.0 * q->N * (K / 64));
-    MING_HIP(profiled(c, q->bits == 4 ? kBF4 : kBF8, flops,
+    MING_HIP(profiled(c, q->bits == 4 ? kBP4 : kBP8, flops,
                       2.0 * M * K + wbytes + 2.0 * M * q->N,
                       [&] { return ming::launch_qproj_pair(q->bits, a, c->stream); }),
              "qproj pair launch");
