@@ -700,32 +700,36 @@ __global__ __launch_bounds__(256, 1) void qproj_pair_kernel(const QprojArgs a) {
 
 // The split projection's end: y = bf16(sum of the slices in order), then as
 // the epilogue: the fused SwiGLU bf16(silu(g) * y) and the fp16 copy.
+// 32-bit indices: the host keeps M * N / 4 below 2^31.
 __global__ void qproj_split_reduce_kernel(const QprojArgs a) {
-  const int n4 = a.N >> 2;
-  const long long total = (long long)a.M * n4;
+  const unsigned n4 = (unsigned)a.N >> 2;
+  const unsigned total = (unsigned)a.M * n4;
+  const size_t plane = (size_t)a.M * (size_t)a.N;
   uint32_t seen = 0;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-       i += (long long)gridDim.x * blockDim.x) {
-    const long long m = i / n4;
-    const int n = (int)(i % n4) * 4;
-    float4 sum = *reinterpret_cast<const float4*>(a.part + m * a.N + n);
+  for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += gridDim.x * blockDim.x) {
+    const unsigned m = i / n4;
+    const unsigned n = (i - m * n4) * 4;
+    const float* p = a.part + (size_t)m * a.N + n;
+    float4 sum = *reinterpret_cast<const float4*>(p);
     for (int k = 1; k < a.kslices; ++k) {
-      const float4 v = *reinterpret_cast<const float4*>(a.part + ((long long)k * a.M + m) * a.N + n);
+      p += plane;
+      const float4 v = *reinterpret_cast<const float4*>(p);
       sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
     }
     uint32_t vp[2] = {pack_bf16x2_rne(sum.x, sum.y), pack_bf16x2_rne(sum.z, sum.w)};
     if (a.g) {
-      const uint2 gv = *reinterpret_cast<const uint2*>(a.g + m * a.ldg + n);
+      const uint2 gv = *reinterpret_cast<const uint2*>(a.g + (size_t)m * a.ldg + n);
       const uint32_t gp[2] = {gv.x, gv.y};
 #pragma unroll
       for (int e = 0; e < 2; ++e)
         vp[e] = pack_bf16x2_rne(silu_f(bf16_lo(gp[e])) * bf16_lo(vp[e]),
                                 silu_f(bf16_hi(gp[e])) * bf16_hi(vp[e]));
     }
-    *reinterpret_cast<uint2*>(a.y + m * a.ldy + n) = make_uint2(vp[0], vp[1]);
+    *reinterpret_cast<uint2*>(a.y + (size_t)m * a.ldy + n) = make_uint2(vp[0], vp[1]);
     if (a.yh) {
       seen = range_track(range_track(seen, vp[0]), vp[1]);
-      *reinterpret_cast<uint2*>(a.yh + m * a.ldyh + n) =
+      *reinterpret_cast<uint2*>(a.yh + (size_t)m * a.ldyh + n) =
           make_uint2(bf16x2_to_f16x2(vp[0]), bf16x2_to_f16x2(vp[1]));
     }
   }
@@ -924,29 +928,44 @@ __global__ __launch_bounds__(512, 1) void lora_xa_fast_kernel(const LoraXaArgs a
 }
 
 // T[m][c] = bf16(coef * sum_s P[s][m][c]), slices summed in order 0..S-1.
+// One thread per 8 columns (one coefficient group): two 16-B loads per
+// slice, one 16-B store when T's rows are 16-B aligned; 32-bit indices (the
+// host keeps M * n_cols / 8 below 2^31).
 __global__ void lora_xa_reduce_kernel(const float* part, int kslices, int M,
                                       int n_cols, const LoraXaArgs a) {
-  const int c4 = n_cols >> 2;
-  const long long total = (long long)M * c4;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-       i += (long long)gridDim.x * blockDim.x) {
-    const long long m = i / c4;
-    const int c = (int)(i % c4) * 4;
-    float4 s = *reinterpret_cast<const float4*>(part + m * n_cols + c);
+  const unsigned c8n = (unsigned)n_cols >> 3;
+  const unsigned total = (unsigned)M * c8n;
+  const size_t plane = (size_t)M * (size_t)n_cols;
+  const bool st16 = (reinterpret_cast<uintptr_t>(a.t) & 15) == 0 && (a.ldt & 7) == 0;
+  for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += gridDim.x * blockDim.x) {
+    const unsigned m = i / c8n;
+    const unsigned c = (i - m * c8n) * 8;
+    const float* p = part + (size_t)m * n_cols + c;
+    float4 s0 = *reinterpret_cast<const float4*>(p);
+    float4 s1 = *reinterpret_cast<const float4*>(p + 4);
     for (int k = 1; k < kslices; ++k) {
-      const float4 v = *reinterpret_cast<const float4*>(
-          part + ((long long)k * M + m) * n_cols + c);
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+      p += plane;
+      const float4 v0 = *reinterpret_cast<const float4*>(p);
+      const float4 v1 = *reinterpret_cast<const float4*>(p + 4);
+      s0.x += v0.x; s0.y += v0.y; s0.z += v0.z; s0.w += v0.w;
+      s1.x += v1.x; s1.y += v1.y; s1.z += v1.z; s1.w += v1.w;
     }
     const float f = a.coef[c >> 3];
-    uint2 o;
-    if (f == 0.0f) {
-      o = make_uint2(0, 0);
-    } else {
-      o.x = pack_bf16x2_rne(f * s.x, f * s.y);
-      o.y = pack_bf16x2_rne(f * s.z, f * s.w);
+    uint4 o = make_uint4(0, 0, 0, 0);
+    if (f != 0.0f) {
+      o.x = pack_bf16x2_rne(f * s0.x, f * s0.y);
+      o.y = pack_bf16x2_rne(f * s0.z, f * s0.w);
+      o.z = pack_bf16x2_rne(f * s1.x, f * s1.y);
+      o.w = pack_bf16x2_rne(f * s1.z, f * s1.w);
     }
-    *reinterpret_cast<uint2*>(a.t + m * a.ldt + c) = o;
+    uint16_t* const tp = a.t + (size_t)m * a.ldt + c;
+    if (st16) {
+      *reinterpret_cast<uint4*>(tp) = o;
+    } else {
+      reinterpret_cast<uint2*>(tp)[0] = make_uint2(o.x, o.y);
+      reinterpret_cast<uint2*>(tp)[1] = make_uint2(o.z, o.w);
+    }
   }
 }
 
@@ -1033,7 +1052,8 @@ hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return hipSuccess;
   if (a.kslices > 1) {
-    if (!a.part || a.N % 4 != 0) return hipErrorInvalidValue;
+    if (!a.part || a.N % 4 != 0 || (long long)a.M * (a.N / 4) >= (1ll << 31))
+      return hipErrorInvalidValue;
     const dim3 grid((unsigned)(tiles * a.kslices));
     if (bits == 4)
       hipLaunchKernelGGL((qproj_fast_kernel<4, true>), grid, dim3(256), 0, s, a);
@@ -1110,11 +1130,13 @@ int dense_xa_slices(int M, int N, int K) {
 hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s) {
   if (a.M <= 0 || a.n_cols <= 0) return hipSuccess;
+  // the reduce's 32-bit indexing: one thread per 8 columns
+  const long long work = (long long)a.M * (a.n_cols / 8);
+  if (kslices > 1 && (a.n_cols % 8 != 0 || work >= (1ll << 31))) return hipErrorInvalidValue;
   const unsigned nblk = (unsigned)(((a.M + 255) / 256) * ((a.n_cols + 127) / 128) * kslices);
   hipLaunchKernelGGL(lora_xa_fast_kernel, dim3(nblk), dim3(512), 0, s, a, part, kslices);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || kslices == 1) return e;
-  long long work = (long long)a.M * (a.n_cols / 4);
   long long blocks = (work + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(lora_xa_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
