@@ -441,6 +441,11 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
     // T region = first 16 KB of the stage buffer, B region = second. A
     // lane's 16 bytes are the 8 ranks of one group; the chunk's four groups
     // are wave-uniform (scalar loads).
+    auto grp_word = [&](int ch) -> uint2 {
+      const int gi = __builtin_amdgcn_readfirstlane(grp0 + 4 * ch);
+      return reinterpret_cast<const uint2*>(a.grp)[gi >> 2];
+    };
+    uint2 gw_next = grp_word(0);
     auto issue_t = [&](int ch, const uint4* X) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -451,18 +456,17 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
           dma16_sb(tu + 32 * ch, toff[i], lds_addr(X + 2048 + 64 * (4 * wave + i)));
       }
       // The chunk's four groups are one aligned 8-byte word of the table (a
-      // segment's groups start at a multiple of 4): a wave-uniform scalar
-      // load (lgkmcnt), never a VMEM load the compiler would wait for with
-      // vmcnt(0) behind the ring's DMAs.
-      const int gi = __builtin_amdgcn_readfirstlane(grp0 + 4 * ch);
-      const uint2 gw = reinterpret_cast<const uint2*>(a.grp)[gi >> 2];
-      int gq[4] = {(int16_t)(gw.x & 0xffffu), (int16_t)(gw.x >> 16),
-                   (int16_t)(gw.y & 0xffffu), (int16_t)(gw.y >> 16)};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) gq[e] = gq[e] < 0 ? g_safe : gq[e];
+      // segment's groups start at a multiple of 4), read by a wave-uniform
+      // scalar load one issue ahead, so no issue waits on it. A lane picks
+      // its group's 16 bits with a select and a shift (no branch).
+      const uint2 gw = gw_next;
+      const int nx = ch + 1 < chunks32 ? ch + 1 : chunks32 - 1;
+      gw_next = grp_word(nx);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int g = bc[i] == 0 ? gq[0] : bc[i] == 1 ? gq[1] : bc[i] == 2 ? gq[2] : gq[3];
+        const uint32_t w = (bc[i] & 2) ? gw.y : gw.x;
+        int g = (int16_t)(w >> ((bc[i] & 1) << 4));
+        g = g < 0 ? g_safe : g;
         dma16_sb(Bp, boff[i] + (uint32_t)g * 16u, lds_addr(X + 1024 + 64 * (4 * wave + i)));
       }
     };
