@@ -53,24 +53,36 @@ def _refused(ctx):
     assert e.value.code == m.ERR_RANGE and "65536" in str(e.value)
 
 
-def test_largest_carried_value_is_not_a_fault(ctx, orc):
+@pytest.mark.parametrize("live", [False, True])
+def test_largest_carried_value_is_not_a_fault(ctx, orc, live):
     """+-65280 (bf16's largest below 2^16) passes through both fp16 routes
-    exactly: no fault, and the result within the bar."""
+    exactly: no fault, and the result within the bar. With a live adapter the
+    fast route's fp16 copy of x is written by the x.A launch (no conversion
+    launch), without one by the conversion kernel."""
     M, N, K = 300, 512, 640
     x = randn(1, (M, K))
     x[::7, ::5] = 65280.0
     x[3::11, 1::9] = -65280.0
     xb = bf16(x)
     pack, w = make_weight(2, N, K, 4)
-    qw = _qw(ctx, pack, 4)
-    ref = orc.proj(xb, w)
+    lo = [(1, make_lora(8, N, K, 32))] if live else []
+    qw = _qw(ctx, pack, 4, lo)
+    sc = [0.0, 0.5] if live else None
+    ref = orc.proj(xb, w, [(A, B, 0.5) for _, (A, B) in lo])
     for route in ("auto", "general"):
         ctx.set_route(route)
         ctx.reset_engagement()
-        y = _lin(ctx, qw, to_dev(xb), M)
+        ctx.set_profiling(True)
+        ctx.profile_collect()
+        y = _lin(ctx, qw, to_dev(xb), M, sc)
         ctx.synchronize()
+        prof = ctx.profile_collect()
+        ctx.set_profiling(False)
         assert ctx.engagement()["range_faults"] == 0
         assert orc.rel_l2(f32(from_dev(y)), ref) <= TOL
+        if route == "auto":
+            assert prof.get("cvt_f16", {}).get("launches", 0) == (0 if live else 1)
+            assert prof.get("lora_xa", {}).get("launches", 0) == (1 if live else 0)
 
 
 @pytest.mark.parametrize("big", [65536.0, -1.0e6, np.inf])

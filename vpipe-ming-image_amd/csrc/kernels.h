@@ -127,6 +127,12 @@ struct LoraXaArgs {
   int ldt;
   int16_t grp[kMaxGroups];
   float coef[kMaxGroups];
+  // optional (fast kernel only): the fp16 copy of x, [M][ldxh], 16-byte
+  // aligned, ldxh % 8 == 0, written by the launch as it stages x (each
+  // element once); range as in QprojArgs
+  uint16_t* xh;
+  long long ldxh;
+  int* range;
 };
 hipError_t launch_lora_xa(const LoraXaArgs& a, hipStream_t s);
 

@@ -819,25 +819,56 @@ __global__ __launch_bounds__(512, 1) void lora_xa_fast_kernel(const LoraXaArgs a
         dma16_sb(a.A[asrc[i]] + (long long)kt * 64, aoff[i],
                  lds_addr(S + 2048 + 64 * (4 * rw + i)));
     };
+    // The fp16 copy of x (a.xh): the column blocks of one row tile and K
+    // slice split its 256 rows, so each element is converted once. Stage t
+    // is converted while it is in LDS (landed at the previous wait, its
+    // buffer rewritten only after the next barrier): lane q takes chunk
+    // q & 7 of rows r0 + q / 8 + 32 j.
+    const int tiles_c = (a.n_cols + 127) / 128, tc = c0 / 128;
+    const int r0 = 256 * tc / tiles_c, r1 = 256 * (tc + 1) / tiles_c;
+    const int q = 64 * rw + lane, qc = q & 7;
+    uint32_t seen = 0;
+    auto convert = [&](int t, const uint4* S) {
+      if (!a.xh) return;
+#pragma unroll 1
+      for (int r = r0 + (q >> 3); r < r1; r += 32) {
+        const uint4 v = S[r * 8 + (qc ^ ((r >> 1) & 7))];
+        if (m0 + r < a.M) {
+          seen = range_track4(seen, v);
+          uint4 f;
+          f.x = bf16x2_to_f16x2(v.x);
+          f.y = bf16x2_to_f16x2(v.y);
+          f.z = bf16x2_to_f16x2(v.z);
+          f.w = bf16x2_to_f16x2(v.w);
+          *reinterpret_cast<uint4*>(a.xh + (long long)(m0 + r) * a.ldxh +
+                                    (long long)(kt0 + t) * 64 + 8 * qc) = f;
+        }
+      }
+    };
     issue(kt0, st0);
     issue(kt0 + (NT > 1 ? 1 : 0), st1);
     ring_wait<PER>();                             // stage 0 landed
-    // stage t: stage t + 2 (a re-read of the last past the end) into the
-    // buffer of stage t - 1, then stage t + 1 landed, then the barrier
-    auto step = [&](int t, const uint4* Pv) {
+    // stage t: the copy of stage t, stage t + 2 (a re-read of the last past
+    // the end) into the buffer of stage t - 1, then stage t + 1 landed, then
+    // the barrier. The copy's stores go before the DMAs: vmcnt counts both
+    // in issue order, so the wait for all but the newest PER (stage t + 2)
+    // also covers the stores, whose latency the MFMA waves' stage hides.
+    auto step = [&](int t, const uint4* C, const uint4* Pv) {
+      convert(t, C);
       issue(kt0 + (t + 2 < NT ? t + 2 : NT - 1), Pv);
       ring_wait<PER>();
     };
     int t = 0;
     for (; t + 3 <= NT; t += 3) {
-      step(t, st2);
-      step(t + 1, st0);
-      step(t + 2, st1);
+      step(t, st0, st2);
+      step(t + 1, st1, st0);
+      step(t + 2, st2, st1);
     }
-    if (NT - t >= 1) step(t, st2);
-    if (NT - t == 2) step(t + 1, st0);
+    if (NT - t >= 1) step(t, st0, st2);
+    if (NT - t == 2) step(t + 1, st1, st0);
     // no DMA outlives the block; no barrier: the MFMA waves meet no more
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (a.xh) range_report(a.range, seen);
     return;
   }
 

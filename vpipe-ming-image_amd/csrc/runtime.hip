@@ -1098,13 +1098,22 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
   }
 
   // ---- launch ------------------------------------------------------------
+  // The fast x.A stages every element of x through LDS: its DMA waves
+  // write the fp16 copy as they go, in place of the conversion launch.
+  const bool xh_in_xa = need_xh && t_cols > 0 && xa_fast;
   if (t_cols > 0) {
     xa.x = x; xa.ldx = ldx; xa.K = K; xa.M = M;
     xa.n_cols = t_cols; xa.t = T; xa.ldt = t_cols;
+    if (xh_in_xa) {
+      xa.xh = const_cast<uint16_t*>(xh);
+      xa.ldxh = K;
+      xa.range = range_word(c);
+    }
     double a_bytes = 0.0;
     for (int i = 0; i < n; ++i)
       if (xa.A[i]) a_bytes += 2.0 * qs[i]->a_rows * (double)K;
-    MING_HIP(profiled(c, kBXa, xa_flops, 2.0 * M * K + a_bytes + 2.0 * M * t_cols,
+    MING_HIP(profiled(c, kBXa, xa_flops,
+                      2.0 * M * K + a_bytes + 2.0 * M * t_cols + (xh_in_xa ? 2.0 * M * K : 0.0),
                       [&] {
                         return xa_fast ? ming::launch_lora_xa_fast(xa, part, xa_ks, c->stream)
                                        : ming::launch_lora_xa(xa, c->stream);
@@ -1112,7 +1121,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
              "lora_xa launch");
     c->eng.lora_xa += 1;
   }
-  if (need_xh) {
+  if (need_xh && !xh_in_xa) {
     uint16_t* dst = const_cast<uint16_t*>(xh);
     MING_HIP(profiled(c, kBCvt, 0.0, 4.0 * M * K,
                       [&] { return ming::launch_bf16_to_f16(x, ldx, dst, K, M, K,
