@@ -361,6 +361,10 @@ def _ffn_four_calls(ctx, w1, w3, w2, x, M, F, scales):
     (300, 256, 320, 8, 8, CFG2_SCALES),     # w8, F not a whole 128-column tile
     (513, 256, 448, 4, 8, None),            # no live adapter: no tail at all
     (260, 384, 640, 4, 6, CFG2_SCALES),     # w3 with fewer tail chunks than w1
+    # 17 x 16 = 272 paired tiles: the second round holds one tile row, which
+    # runs as 128-row tiles in a launch of its own
+    (4352, 256, 2048, 4, 8, CFG2_SCALES),
+    (4300, 256, 2048, 8, 8, CFG2_SCALES),   # w8, the half-tile rows ragged
 ])
 def test_ffn_equals_the_four_calls(ctx, orc, M, H, F, bits, w3_slots, scales):
     """ming_ffn == lin(w1), lin(w3), swiglu, lin(w2) bit for bit, h included.

@@ -160,17 +160,20 @@ __device__ __forceinline__ int wchunk(int n, int h) {
 // gate weight (waves 0-1) and the same 128 rows of the up weight (waves
 // 2-3); the tail stages the gate's and the up projection's T chunks side by
 // side; the epilogue meets the two in LDS and writes only the SwiGLU.
-template <int BITS, bool SPLIT, bool PAIR>
+template <int BITS, bool SPLIT, bool PAIR, int RF>
 __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
   constexpr int WCH = BITS == 4 ? 512 : 1024;    // 16-B code chunks per stage
   constexpr int CPR = BITS == 4 ? 2 : 4;         // code chunks per row
   constexpr int WDMA = WCH / 256;                // code DMAs per wave per stage
-  constexpr int PER = 8 + WDMA + 1;              // DMAs per wave per base stage
-  constexpr int TPER = PAIR ? 12 : 8;            // DMAs per wave per tail chunk
+  constexpr int BMT = 32 * RF;                   // rows per tile: RF fragments of 32
+  constexpr int XD = RF;                         // x DMAs per wave per stage
+  constexpr int TD = RF / 2;                     // T DMAs per wave per tail chunk
+  constexpr int PER = XD + WDMA + 1;             // DMAs per wave per base stage
+  constexpr int TPER = (PAIR ? 2 : 1) * TD + 4;  // DMAs per wave per tail chunk
   constexpr int BNT = PAIR ? BN / 2 : BN;        // output columns per tile
   // One __shared__ object per stage: [x 32 KB | codes | (s, b)]; a tail
   // chunk is [T 16 KB | B 16 KB (| the up projection's T 16 KB)].
-  constexpr int STG0 = BM * 8 + WCH + BN / 4;
+  constexpr int STG0 = BMT * 8 + WCH + BN / 4;
   constexpr int STG = PAIR && STG0 < 3072 ? 3072 : STG0;
   __shared__ uint4 st0[STG], st1[STG], st2[STG];
 
@@ -185,7 +188,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
   const bool upw = PAIR && wave >= 2;
   const int wcol = PAIR ? 64 * (wave & 1) : 64 * wave;
 
-  const int tiles_m = (a.M + BM - 1) / BM;
+  const int tiles_m = (a.M + BMT - 1) / BMT;
   const int tiles_n = (a.N + BNT - 1) / BNT;
   int tm, tn, blk = (int)blockIdx.x, ks = 0, kt0 = 0;
   int KT = a.K / BK;
@@ -196,7 +199,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
     KT = KT * (ks + 1) / a.kslices - kt0;
   }
   tile_of_block(blk, tiles_m, tiles_n, &tm, &tn);
-  const int m0 = tm * BM, n0 = tn * BNT;
+  const int m0 = tm * BMT, n0 = tn * BNT;
   const int mlast = a.M - 1, nlast = a.N - 1;
 
   // stage 0 of this block's K range
@@ -209,10 +212,10 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
   // x tile: wave issues chunks q = 8*wave + i; lane p = 64q + lane.
   // Byte offsets from the stage's base (the host keeps every tile inside
   // 4 GiB of its base, so they fit 32 bits).
-  uint32_t xoff[8];
+  uint32_t xoff[XD];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int p = 64 * (8 * wave + i) + lane;
+  for (int i = 0; i < XD; ++i) {
+    const int p = 64 * (XD * wave + i) + lane;
     const int row = p >> 3;
     const int c = (p & 7) ^ ((row >> 1) & 7);
     int m = m0 + row;
@@ -240,23 +243,23 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
     if (g < 2) {
       const void* base = x16 + (long long)kt * BK;
 #pragma unroll
-      for (int i = 4 * g; i < 4 * g + 4; ++i)
-        dma16_sb(base, xoff[i], lds_addr(B + 64 * (8 * wave + i)));
+      for (int i = (XD / 2) * g; i < (XD / 2) * (g + 1); ++i)
+        dma16_sb(base, xoff[i], lds_addr(B + 64 * (XD * wave + i)));
     } else {
       const void* wbase = codes + (long long)kt * a.N * CPR;
 #pragma unroll
       for (int i = 0; i < WDMA; ++i)
-        dma16_sb(wbase, woff[i], lds_addr(B + BM * 8 + 64 * (WDMA * wave + i)));
+        dma16_sb(wbase, woff[i], lds_addr(B + BMT * 8 + 64 * (WDMA * wave + i)));
       dma4_sb(sbp + (long long)kt * a.N, soff,
-              lds_addr(reinterpret_cast<const uint32_t*>(B + BM * 8 + WCH) + 64 * wave));
+              lds_addr(reinterpret_cast<const uint32_t*>(B + BMT * 8 + WCH) + 64 * wave));
     }
   };
 
-  floatx16_t acc[2][8];
+  floatx16_t acc[2][RF];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < RF; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
 
@@ -264,12 +267,12 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
   // n-tiles, and the current k16 step's operands.
   uint4 wc[2][CPR / 2];
   half2v s2[2], b2[2];
-  uint4 wa[2], xb[8];
+  uint4 wa[2], xb[RF];
 
   auto load_ws = [&](const uint4* B, uint4 (&wcv)[2][CPR / 2], half2v (&s2v)[2],
                      half2v (&b2v)[2]) {
-    const uint4* W = B + BM * 8;
-    const uint32_t* S = reinterpret_cast<const uint32_t*>(B + BM * 8 + WCH);
+    const uint4* W = B + BMT * 8;
+    const uint32_t* S = reinterpret_cast<const uint32_t*>(B + BMT * 8 + WCH);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int n = 64 * wave + 32 * j + fr;
@@ -306,24 +309,24 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
     const int nk = kt + 2 < KT ? kt + 2 : KT - 1;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      uint4 wn_[2], xn_[8];
+      uint4 wn_[2], xn_[RF];
       uint4 wcn[2][CPR / 2];
       half2v s2n[2], b2n[2];
       if (kk < 3) {
         issue_grp(kk, nk, Pv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xn_[i] = C[swz8(32 * i + fr, 2 * (kk + 1) + fk)];
+        for (int i = 0; i < RF; ++i) xn_[i] = C[swz8(32 * i + fr, 2 * (kk + 1) + fk)];
 #pragma unroll
         for (int j = 0; j < 2; ++j) wn_[j] = deq(wc, s2, b2, j, kk + 1);
       } else {
         load_ws(Nx, wcn, s2n, b2n);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xn_[i] = Nx[swz8(32 * i + fr, fk)];
+        for (int i = 0; i < RF; ++i) xn_[i] = Nx[swz8(32 * i + fr, fk)];
 #pragma unroll
         for (int j = 0; j < 2; ++j) wn_[j] = deq(wcn, s2n, b2n, j, 0);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < RF; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
@@ -331,30 +334,34 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
               acc[j][i], 0, 0, 0);
       if (kk < 3) {
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
+        for (int g = 0; g < RF; ++g) {
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
         }
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // 4 VALU
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        for (int g = 0; g < RF; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 32 / RF, 0);   // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
         }
       } else {
-        constexpr int NDS = 8 + 2 * (CPR / 2) + 2;
-        static_assert(NDS >= 10 && NDS <= 20, "step-3 DS reads per MFMA pin");
+        // step 3: NDS reads over the DSM MFMAs left after the VG that carry
+        // the next stage's first dequantization
+        constexpr int NDS = RF + 2 * (CPR / 2) + 2;
+        constexpr int VG = 3 * RF / 4;
+        constexpr int DSM = 2 * RF - VG;
+        static_assert(NDS >= DSM && NDS <= 2 * DSM, "step-3 DS reads per MFMA pin");
 #pragma unroll
-        for (int g = 0; g < NDS - 10; ++g) {
+        for (int g = 0; g < NDS - DSM; ++g) {
           __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
 #pragma unroll
-        for (int g = NDS - 10; g < 10; ++g) {
+        for (int g = NDS - DSM; g < DSM; ++g) {
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
 #pragma unroll
-        for (int g = 0; g < 6; ++g) {
+        for (int g = 0; g < VG; ++g) {
           __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
@@ -367,7 +374,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) wa[j] = wn_[j];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) xb[i] = xn_[i];
+      for (int i = 0; i < RF; ++i) xb[i] = xn_[i];
       if (kk == 3) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -388,7 +395,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
   ring_wait<PER>();
   load_ws(st0, wc, s2, b2);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) xb[i] = st0[swz8(32 * i + fr, fk)];
+  for (int i = 0; i < RF; ++i) xb[i] = st0[swz8(32 * i + fr, fk)];
 #pragma unroll
   for (int j = 0; j < 2; ++j) wa[j] = deq(wc, s2, b2, j, 0);
 
@@ -422,21 +429,44 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
     // the first live group of the segment: a finite source for padding
     // groups (their T columns are exactly 0)
     const int g_safe = a.grp[grp0];
-    uint32_t toff[4];
+    // T: BMT rows x 4 chunks (TD DMAs a wave); B: 256 rows x 4 chunks (4)
+    uint32_t toff[TD];
     uint32_t boff[4];
     int bc[4];
+    if constexpr (TD == 4) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = 64 * (4 * wave + i) + lane;
-      const int row = p >> 2;
-      const int c = (p & 3) ^ ((row >> 2) & 3);
-      int m = m0 + row;
-      m = m < mlast ? m : mlast;
-      toff[i] = (uint32_t)(((long long)m * a.ldt + t_col0 + 8 * c) * 2);
-      int n = n0 + (PAIR ? (row & 127) : row);
-      n = n < seg_ne - 1 ? n : seg_ne - 1;
-      boff[i] = (uint32_t)((long long)(n - seg_nb) * ldb * 2);
-      bc[i] = c;
+      for (int i = 0; i < 4; ++i) {
+        const int p = 64 * (4 * wave + i) + lane;
+        const int row = p >> 2;
+        const int c = (p & 3) ^ ((row >> 2) & 3);
+        int m = m0 + row;
+        m = m < mlast ? m : mlast;
+        toff[i] = (uint32_t)(((long long)m * a.ldt + t_col0 + 8 * c) * 2);
+        int n = n0 + (PAIR ? (row & 127) : row);
+        n = n < seg_ne - 1 ? n : seg_ne - 1;
+        boff[i] = (uint32_t)((long long)(n - seg_nb) * ldb * 2);
+        bc[i] = c;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TD; ++i) {
+        const int p = 64 * (TD * wave + i) + lane;
+        const int row = p >> 2;
+        const int c = (p & 3) ^ ((row >> 2) & 3);
+        int m = m0 + row;
+        m = m < mlast ? m : mlast;
+        toff[i] = (uint32_t)(((long long)m * a.ldt + t_col0 + 8 * c) * 2);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = 64 * (4 * wave + i) + lane;
+        const int row = p >> 2;
+        const int c = (p & 3) ^ ((row >> 2) & 3);
+        int n = n0 + (PAIR ? (row & 127) : row);
+        n = n < seg_ne - 1 ? n : seg_ne - 1;
+        boff[i] = (uint32_t)((long long)(n - seg_nb) * ldb * 2);
+        bc[i] = c;
+      }
     }
     // T region = first 16 KB of the stage buffer, B region = second. A
     // lane's 16 bytes are the 8 ranks of one group; the chunk's four groups
@@ -448,12 +478,12 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
     uint2 gw_next = grp_word(0);
     auto issue_t = [&](int ch, const uint4* X) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dma16_sb(a.t + 32 * ch, toff[i], lds_addr(X + 64 * (4 * wave + i)));
+      for (int i = 0; i < TD; ++i)
+        dma16_sb(a.t + 32 * ch, toff[i], lds_addr(X + 64 * (TD * wave + i)));
       if constexpr (PAIR) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          dma16_sb(tu + 32 * ch, toff[i], lds_addr(X + 2048 + 64 * (4 * wave + i)));
+        for (int i = 0; i < TD; ++i)
+          dma16_sb(tu + 32 * ch, toff[i], lds_addr(X + 2048 + 64 * (TD * wave + i)));
       }
       // The chunk's four groups are one aligned 8-byte word of the table (a
       // segment's groups start at a multiple of 4), read by a wave-uniform
@@ -470,14 +500,14 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
         dma16_sb(Bp, boff[i] + (uint32_t)g * 16u, lds_addr(X + 1024 + 64 * (4 * wave + i)));
       }
     };
-    uint4 ta[2], tb[8];
-    auto read_t = [&](const uint4* X, int kk, uint4 (&av)[2], uint4 (&bv)[8]) {
+    uint4 ta[2], tb[RF];
+    auto read_t = [&](const uint4* X, int kk, uint4 (&av)[2], uint4 (&bv)[RF]) {
       const int c = 2 * kk + fk;
 #pragma unroll
       for (int j = 0; j < 2; ++j) av[j] = X[1024 + swz4(64 * wave + 32 * j + fr, c)];
       const uint4* const XT = upw ? X + 2048 : X;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) bv[i] = XT[swz4(32 * i + fr, c)];
+      for (int i = 0; i < RF; ++i) bv[i] = XT[swz4(32 * i + fr, c)];
     };
     // Chunk ch: step 0 reads step 1's fragments and issues chunk ch+2 into
     // Pv; the wait + barrier sit between the steps; step 1 reads the next
@@ -486,7 +516,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
       const int nc = ch + 2 < chunks32 ? ch + 2 : chunks32 - 1;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        uint4 an[2], bn[8];
+        uint4 an[2], bn[RF];
         if (kk == 0) {
           issue_t(nc, Pv);
           read_t(C, 1, an, bn);
@@ -494,14 +524,14 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
           read_t(Nx, 0, an, bn);
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < RF; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                 __builtin_bit_cast(bf16x8_t, ta[j]), __builtin_bit_cast(bf16x8_t, tb[i]),
                 acc[j][i], 0, 0, 0);
 #pragma unroll
-        for (int g = 0; g < 10; ++g) {
+        for (int g = 0; g < 2 + RF; ++g) {
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
         }
@@ -513,7 +543,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) ta[j] = an[j];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) tb[i] = bn[i];
+        for (int i = 0; i < RF; ++i) tb[i] = bn[i];
       }
     };
     issue_t(0, st0);
@@ -534,7 +564,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
   if constexpr (SPLIT) {
     // f32 partials P[ks][m][n]: lane row 32i + fr, four columns per quad
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < RF; ++i) {
       const int m = m0 + 32 * i + fr;
       if (m >= a.M) continue;
 #pragma unroll
@@ -565,7 +595,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
     const int n = n0 + wcol + 8 * cl;
     uint32_t seen = 0;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < RF / 4; ++h) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int i = 4 * h + ii;
@@ -626,7 +656,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
   const int n = n0 + 64 * wave + 8 * cl;
   uint32_t seen = 0;   // magnitudes written to the fp16 copy (range_report)
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < RF / 4; ++h) {
     // Fused SwiGLU: this half's gate rows are loaded first, so their memory
     // latency overlaps the conversion below instead of stalling each store.
     uint4 gv[16];
@@ -694,12 +724,14 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
 
 template <int BITS, bool SPLIT>
 __global__ __launch_bounds__(256, 1) void qproj_fast_kernel(const QprojArgs a) {
-  qproj_fast_body<BITS, SPLIT, false>(a);
+  qproj_fast_body<BITS, SPLIT, false, 8>(a);
 }
 
-template <int BITS>
+// RF = 8: 256-row tiles; RF = 4: 128-row tiles (the rows of a grid's last,
+// mostly empty round, see launch_qproj_pair)
+template <int BITS, int RF>
 __global__ __launch_bounds__(256, 1) void qproj_pair_kernel(const QprojArgs a) {
-  qproj_fast_body<BITS, false, true>(a);
+  qproj_fast_body<BITS, false, true, RF>(a);
 }
 
 // The split projection's end: y = bf16(sum of the slices in order), then as
@@ -1112,19 +1144,62 @@ hipError_t launch_qproj_fast(int bits, const QprojArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// CUs of the current device (the launch rounds are counted against it).
+static int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// A grid whose last round of the chip's CUs holds at most one row of tiles
+// (4352 rows: 1360 tiles, 80 in a sixth round on 256 CUs) runs that tile
+// row as 128-row tiles in a second launch over the same arguments shifted
+// down: twice the blocks at about half the time each. Each output element
+// is computed by the same MFMA sequence either way, so the bits do not
+// depend on the split.
 hipError_t launch_qproj_pair(int bits, const QprojArgs& a, hipStream_t s) {
-  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN / 2 - 1) / (BN / 2));
+  const int tiles_n = (a.N + BN / 2 - 1) / (BN / 2);
+  const int tiles_m = (a.M + BM - 1) / BM;
+  const int tiles = tiles_m * tiles_n;
   if (tiles <= 0) return hipSuccess;
   if (a.kslices > 1 || a.g || !a.codes_u || !a.sb_u || a.nseg != 1 ||
       a.seg[0].chunks != a.seg_u.chunks || a.N % 8 != 0 || a.ldy % 8 != 0 ||
-      (reinterpret_cast<uintptr_t>(a.y) & 15) != 0)
+      (reinterpret_cast<uintptr_t>(a.y) & 15) != 0 || (bits != 4 && bits != 8))
     return hipErrorInvalidValue;
+  const int cus = device_cus();
+  const int excess = tiles % cus;
+  const int rows_main =
+      (tiles_m >= 2 && tiles > cus && excess > 0 && excess <= tiles_n) ? (tiles_m - 1) * BM : a.M;
+  {
+    QprojArgs m = a;
+    m.M = rows_main;
+    const dim3 grid((unsigned)(tiles_m - (rows_main < a.M ? 1 : 0)) * tiles_n);
+    if (bits == 4)
+      hipLaunchKernelGGL((qproj_pair_kernel<4, 8>), grid, dim3(256), 0, s, m);
+    else
+      hipLaunchKernelGGL((qproj_pair_kernel<8, 8>), grid, dim3(256), 0, s, m);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || rows_main == a.M) return e;
+  }
+  QprojArgs h = a;
+  h.M = a.M - rows_main;
+  h.x = a.x + (long long)rows_main * a.ldx;
+  h.y = a.y + (long long)rows_main * a.ldy;
+  if (a.yh) h.yh = a.yh + (long long)rows_main * a.ldyh;
+  if (a.t) h.t = a.t + (long long)rows_main * a.ldt;
+  const dim3 grid((unsigned)(((h.M + BM / 2 - 1) / (BM / 2)) * tiles_n));
   if (bits == 4)
-    hipLaunchKernelGGL((qproj_pair_kernel<4>), dim3(tiles), dim3(256), 0, s, a);
-  else if (bits == 8)
-    hipLaunchKernelGGL((qproj_pair_kernel<8>), dim3(tiles), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((qproj_pair_kernel<4, 4>), grid, dim3(256), 0, s, h);
   else
-    return hipErrorInvalidValue;
+    hipLaunchKernelGGL((qproj_pair_kernel<8, 4>), grid, dim3(256), 0, s, h);
   return hipGetLastError();
 }
 
