@@ -20,6 +20,11 @@
 // Every stage buffer is its own __shared__ object so the compiler's LDS-DMA
 // tracking sees that reads of one stage do not alias the DMA into another.
 //
+// The same body also runs as qproj_pair_kernel (a SwiGLU's gate and up
+// projections in one tile, 128 columns of each) and, for the last tile row
+// of a paired grid whose last round would hold only that row, with 128-row
+// tiles (4 row fragments a wave instead of 8).
+//
 // Resident code layout this kernel reads (built by repack_*_fast):
 //   w4: codes[kt][n][fk][kk]   one u32 = the 8 codes of k = 16kk + 8fk + 0..7,
 //       nibbles ordered {k0,k4,k1,k5,k2,k6,k3,k7} so w & 0x0F0F0F0F holds
