@@ -1164,10 +1164,10 @@ static int device_cus() {
   return cached[dev];
 }
 
-// A grid whose last round of the chip's CUs holds at most one row of tiles
-// (4352 rows: 1360 tiles, 80 in a sixth round on 256 CUs) runs that tile
-// row as 128-row tiles in a second launch over the same arguments shifted
-// down: twice the blocks at about half the time each. Each output element
+// A grid whose last round of the chip's CUs is mostly empty (4352 rows: 1360
+// tiles, 80 in a sixth round on 256 CUs) runs its last tile row as 128-row
+// tiles in a second launch over the same arguments shifted down: twice the
+// blocks at about half the time each. Each output element
 // is computed by the same MFMA sequence either way, so the bits do not
 // depend on the split.
 hipError_t launch_qproj_pair(int bits, const QprojArgs& a, hipStream_t s) {
@@ -1179,10 +1179,18 @@ hipError_t launch_qproj_pair(int bits, const QprojArgs& a, hipStream_t s) {
       a.seg[0].chunks != a.seg_u.chunks || a.N % 8 != 0 || a.ldy % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(a.y) & 15) != 0 || (bits != 4 && bits != 8))
     return hipErrorInvalidValue;
+  // Rounds of the chip, one 256-row tile a CU: the whole grid against the
+  // grid without its last tile row plus that row as 128-row tiles (about
+  // 0.55 of a round each, measured); split when that saves a fifth of a
+  // round or more.
   const int cus = device_cus();
-  const int excess = tiles % cus;
+  const int main_tiles = tiles - tiles_n;
+  const int half_blocks = ((a.M - (tiles_m - 1) * BM + BM / 2 - 1) / (BM / 2)) * tiles_n;
+  const double rounds_whole = (double)((tiles + cus - 1) / cus);
+  const double rounds_split =
+      (double)((main_tiles + cus - 1) / cus) + 0.55 * (double)((half_blocks + cus - 1) / cus);
   const int rows_main =
-      (tiles_m >= 2 && tiles > cus && excess > 0 && excess <= tiles_n) ? (tiles_m - 1) * BM : a.M;
+      (tiles_m >= 2 && rounds_split + 0.2 <= rounds_whole) ? (tiles_m - 1) * BM : a.M;
   {
     QprojArgs m = a;
     m.M = rows_main;
