@@ -1301,6 +1301,10 @@ hipError_t validate_qproj_fast_kernels() {
                        reinterpret_cast<const void*>(&repack_fast_kernel),
                        reinterpret_cast<const void*>(&repack_sbf_kernel),
                        reinterpret_cast<const void*>(&bf16_to_f16_kernel),
+                       reinterpret_cast<const void*>(&qproj_pair_kernel<4, 8>),
+                       reinterpret_cast<const void*>(&qproj_pair_kernel<8, 8>),
+                       reinterpret_cast<const void*>(&qproj_pair_kernel<4, 4>),
+                       reinterpret_cast<const void*>(&qproj_pair_kernel<8, 4>),
                        reinterpret_cast<const void*>(&lora_xa_fast_kernel),
                        reinterpret_cast<const void*>(&lora_xa_reduce_kernel)};
   for (const void* f : fns) {
