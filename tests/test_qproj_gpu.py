@@ -101,6 +101,31 @@ def test_lora_eight_slots_parity(ctx, orc, bits, M, N, K):
     assert orc.rel_l2(ref, base) > 10 * TOL
 
 
+@pytest.mark.parametrize("bits,K", [(4, 64), (4, 128), (4, 192), (8, 64)])
+def test_short_k_parity(ctx, orc, bits, K):
+    """One, two and three 64-wide K stages (the ring's prologue and its
+    remainder stages with no full trip) on a 64-tile grid, so the unsplit
+    fast kernel runs, followed by the 8-chunk LoRA tail of config 2's set."""
+    M, N = 2048, 2048
+    print(f"case short K bits={bits} M={M} N={N} K={K}", flush=True)
+    x = bf16(randn(31 + K, (M, K)))
+    pack, w = make_weight(32 + K, N, K, bits)
+    qw = _qw(ctx, pack, bits)
+    loras = []
+    for s, r in enumerate(CFG2_RANKS):
+        A, B = make_lora(300 + 2 * s, N, K, r)
+        qw.bind_lora(s, A, B)
+        loras.append((A, B, CFG2_SCALES[s]))
+    ctx.reset_engagement()
+    y = _run(ctx, qw, to_dev(x), M, CFG2_SCALES)
+    eng = ctx.engagement()
+    assert eng["lora_proj"] == 1 and eng["gemm_split"] == 0
+    assert eng["gemm_fast"] == (1 if route_is_auto(ctx) else 0)
+    ref = orc.proj(x, w, loras)
+    assert _rel(orc, y, ref) <= TOL
+    assert orc.rel_l2(ref, orc.proj(x, w)) > 10 * TOL
+
+
 ODD_RANKS = (3, 12, 20, 5, 36, 1, 7, 9)
 ODD_SCALES = (0.9, -0.6, 0.4, 1.3, 0.25, -1.1, 0.0, 0.7)
 
@@ -365,6 +390,10 @@ def _ffn_four_calls(ctx, w1, w3, w2, x, M, F, scales):
     # runs as 128-row tiles in a launch of its own
     (4352, 256, 2048, 4, 8, CFG2_SCALES),
     (4300, 256, 2048, 8, 8, CFG2_SCALES),   # w8, the half-tile rows ragged
+    # one and two 64-wide K stages in the paired launch (its ring's
+    # prologue and remainder with no full trip)
+    (4352, 64, 2048, 4, 8, CFG2_SCALES),
+    (4352, 128, 2048, 4, 8, CFG2_SCALES),
 ])
 def test_ffn_equals_the_four_calls(ctx, orc, M, H, F, bits, w3_slots, scales):
     """ming_ffn == lin(w1), lin(w3), swiglu, lin(w2) bit for bit, h included.
