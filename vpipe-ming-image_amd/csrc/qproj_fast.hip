@@ -350,9 +350,12 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
         }
       } else {
         // step 3: NDS reads over the DSM MFMAs left after the VG that carry
-        // the next stage's first dequantization
+        // the next stage's first dequantization (w4 at 256 rows: spread
+        // over 10 MFMAs, 4 VALU each, which measured ~0.5% faster launches
+        // than 6 MFMAs of 6; the reads then go two per MFMA)
         constexpr int NDS = RF + 2 * (CPR / 2) + 2;
-        constexpr int VG = 3 * RF / 4;
+        constexpr int VG = RF == 8 && CPR == 2 ? RF + 2 : 3 * RF / 4;
+        constexpr int VPG = RF == 8 && CPR == 2 ? 4 : 6;   // VALU per group
         constexpr int DSM = 2 * RF - VG;
         static_assert(NDS >= DSM && NDS <= 2 * DSM, "step-3 DS reads per MFMA pin");
 #pragma unroll
@@ -367,7 +370,7 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
         }
 #pragma unroll
         for (int g = 0; g < VG; ++g) {
-          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, VPG, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
       }
