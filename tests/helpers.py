@@ -9,6 +9,10 @@ import oracle as orc
 # BASELINE config 2's adapter set.
 CFG2_RANKS = (4, 8, 16, 16, 32, 32, 64, 128)
 CFG2_SCALES = (1.0, 0.5, 0.0, -0.3, 0.8, 0.0, 1.2, 0.25)
+# BASELINE config 5's set: eight rank-64 slots, strengths uniform in [-1, 1.5]
+# (the draw the bench's CFG run uses).
+CFG5_RANKS = (64,) * 8
+CFG5_SCALES = tuple(float(v) for v in np.random.default_rng(5).uniform(-1.0, 1.5, 8))
 
 
 def randn(seed: int, shape, std: float = 1.0) -> np.ndarray:

@@ -1,10 +1,12 @@
 """BASELINE configs[3] and configs[4] at full size (16640-token joint sequences,
 all 34 blocks, 238 adapted modules).
 
-configs[3]'s velocity is held against an fp32 reference of the whole forward
+Each config's velocity is held against an fp32 reference of the whole forward
 (tests/torch_ref.py on the GPU, pinned to the CPU oracle at reduced width) by
-the reference's own rule for its real-size check (ming-dit-test.cc:2107-2131):
-within twice the distance of a bf16 run from f32, floored at kSmallTol = 0.035.
+the reference's own rule for its real-size check (ming-dit-test.cc:2107-2131)
+and its w8 check (ming-quant-test.cc:826-831): within twice the distance of a
+bf16 run from f32, floored at kSmallTol = 0.035 -- configs[3] (w4) at one
+sigma, configs[4] (w8, eight rank-64 slots) on both forwards of its CFG pair.
 Both configs are also held to the size-independent properties the reference's
 own tests state (ming-dit-test.cc:1249-1273, 2030-2035):
   * strengths changed between forwards and changed back give identical bits;
@@ -98,18 +100,57 @@ def test_config4_forward_2048_strengths_live(ctx):
 
 
 def test_config5_cfg_denoise_2048(ctx):
+    """the w8g64 model with eight rank-64 slots at strengths
+    uniform in [-1, 1.5] (512 live ranks on all 238 modules: 16-chunk tails
+    on the w8 paired and unsplit kernels). Its CFG pair of forwards (the
+    caption, then the all-zero negative of the same shape, as the denoise
+    loop wires it) at a sigma of the shift-6 schedule is held to the fp32
+    reference by the reference's w8 rule, max(0.035, 2 x the bf16 run)
+    (ming-quant-test.cc:826-831); then the 2-step CFG loop is deterministic,
+    finite and moved by guidance."""
     import torch
     import ming_dit_amd as m
+    import torch_ref as tr
+    from helpers import CFG5_RANKS, CFG5_SCALES
     bench = _bench()
     gen = torch.Generator(device="cuda").manual_seed(43)
-    ranks = (64,) * 8
-    scales = tuple(float(v) for v in np.random.default_rng(5).uniform(-1.0, 1.5, 8))
-    model = bench.build_forward_model(ctx, m, torch, gen, bits=8, ranks=ranks)
-    for i, s in enumerate(scales):
+    ref = {}
+    model = bench.build_forward_model(ctx, m, torch, gen, bits=8, ranks=CFG5_RANKS, ref=ref)
+    for i, s in enumerate(CFG5_SCALES):
         model.set_lora_scale(i, s)
     img, cap, pos = bench.layout_2048()
     capt = torch.randn((cap, 2560), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
     noise = torch.randn((img, 64), generator=gen, device="cuda").float().cpu().numpy()
+    sigma = float(orc.schedule_sigmas(11, 6.0)[5])
+    lat = torch.from_numpy(noise).cuda().to(torch.bfloat16).view(torch.int16)
+    zero = torch.zeros_like(capt)
+    c, s = orc.rope_table(*pos)
+    tin = orc.time_proj(sigma, 1000.0, 256)
+    model.set_caption_cache(False)
+    for name, cp in (("positive", capt), ("zero negative", zero)):
+        ctx.reset_engagement()
+        out = torch.empty((img, 64), dtype=torch.int16, device="cuda")
+        torch.cuda.synchronize()
+        assert model.forward(lat, cp, 2560, img, cap, cap, *pos, sigma, out)
+        torch.cuda.synchronize()
+        eng = ctx.engagement()
+        assert eng["gemm_q8"] == 270 and eng["lora_proj"] == 238
+        a = from_dev(out)
+        assert np.isfinite(f32(a)).all()
+        outs = {mode: tr.Ref(mode, "cuda").forward(ref, lat, cp, img, cap, cap, c, s, sigma,
+                                                   CFG5_SCALES, tin)
+                for mode in ("f32", "bf16")}
+        torch.cuda.synchronize()
+        got = torch.from_numpy(f32(a)).cuda()
+        rel = tr.rel_l2(got, outs["f32"])
+        bf_floor = tr.rel_l2(outs["bf16"], outs["f32"])
+        bar = max(0.035, 2 * bf_floor)
+        print(f"configs[4] w8 {name} velocity vs fp32: {rel:.3e} (bf16 run {bf_floor:.3e}, "
+              f"bar {bar:.3e}); vs the bf16 run {tr.rel_l2(got, outs['bf16']):.3e}", flush=True)
+        assert rel <= bar
+        del outs, got
+    del ref
+    model.set_caption_cache(True)
     x1, x2 = noise.copy(), noise.copy()
     ctx.reset_engagement()
     assert model.denoise(x1, capt, 2560, cap, cap, pos, img, 2, 6.0, 4.0)

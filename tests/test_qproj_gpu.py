@@ -8,8 +8,9 @@ import numpy as np
 import pytest
 
 import ming_dit_amd as m
-from helpers import (CFG2_RANKS, CFG2_SCALES, bf16, empty_bf16, from_dev,
-                     make_lora, make_weight, randn, sync, to_dev)
+from helpers import (CFG2_RANKS, CFG2_SCALES, CFG5_RANKS, CFG5_SCALES, bf16,
+                     empty_bf16, from_dev, make_lora, make_weight, randn, sync,
+                     to_dev)
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -597,39 +598,38 @@ def _cfg2_rows(M, tile=256):
     return np.array(sorted(set(rows)), np.int64)
 
 
-def test_config2_ffn_full_size(ctx, orc):
-    """BASELINE configs[1] exactly: X [4352, 3840] ~ N(0, 1) bf16, w1/w3
-    3840 -> 10240 and w2 10240 -> 3840 as w4g64 packs of N(0, 0.02) weights,
-    the eight slots {4, 8, 16, 16, 32, 32, 64, 128} at strengths
-    {1, .5, 0, -.3, .8, 0, 1.2, .25} on all three, through ming_ffn (the
-    bench's step). On the fast route w1 and w3 run as one paired launch
-    (17 x 80 tiles of 128 columns of each, the SwiGLU taken in LDS) and w2 as
-    the unsplit w4 kernel (17 x 15 tiles), each with the 8-chunk tail. On a
-    row sample over
-    all 17 M tiles, against the oracle (gpu_ff, ming-dit.cc:2151-2162):
-      h (w3's fused epilogue) vs swiglu(bf16(x.W1'), bf16(x.W3')) and y vs
-      the f32 reference of w2 on the kernel's own h: each stage on its own
-      input, to the projection bar (2e-3);
-      y vs the oracle's whole chain (w2 over the oracle's h): two stages
-      that each round to bf16, so 1-ulp flips of g and u where the GPU's f32
-      sum and the oracle's f64 one straddle a rounding boundary carry into
-      w2's input. Independent stage errors add in quadrature: sqrt(2) x the
-      bar (measured 2.05e-3)."""
+def _ffn_full_size(ctx, orc, bits, ranks, scales, seed, label):
+    """One block's SwiGLU FFN at the configs' full size through ming_ffn (the
+    bench's step): X [4352, 3840] ~ N(0, 1) bf16, w1/w3 3840 -> 10240 and w2
+    10240 -> 3840 as w{bits}g64 packs of N(0, 0.02) weights, the adapter set
+    (ranks, strengths) on all three. On the fast route w1 and w3 run as one
+    paired launch (17 x 80 tiles of 128 columns of each, the SwiGLU taken in
+    LDS) and w2 as the unsplit kernel (17 x 15 tiles), each with the tail of
+    the live ranks in 32-rank chunks. Held on a row sample over all 17 M tiles
+    against the oracle (gpu_ff, ming-dit.cc:2151-2162):
+      * each stage on its own input, to the projection bar (2e-3): h (w3's
+        fused epilogue) vs swiglu(bf16(x.W1'), bf16(x.W3')), and y vs the
+        f32 w2 on the kernel's own h;
+      * the whole chain by the reference's rule for a result that passes
+        through more than one bf16 rounding (ming-dit-test.cc:2125-2131;
+        ming-quant-test.cc:826-831): y within twice the distance of the
+        bf16-rounded oracle chain (g, u, h and y each rounded) from the f32
+        chain (nothing rounded), floored at the projection bar."""
     M, H, F = 4352, 3840, 10240
-    x = bf16(randn(2001, (M, H)))
+    x = bf16(randn(seed + 1, (M, H)))
     packs, loras = [], []
     for i, (N, K) in enumerate(((F, H), (F, H), (H, F))):
-        codes, sc, bi = orc.quantize(randn(2010 + i, (N, K), 0.02), 4)
+        codes, sc, bi = orc.quantize(randn(seed + 10 + i, (N, K), 0.02), bits)
         packs.append((codes, sc, bi))
         lo = []
-        for s, r in enumerate(CFG2_RANKS):
-            A = bf16(randn(2100 + 20 * i + 2 * s, (r, K), 1.0 / np.sqrt(K)))
-            B = bf16(randn(2101 + 20 * i + 2 * s, (N, r), 0.01))
-            lo.append((A, B, CFG2_SCALES[s]))
+        for s, r in enumerate(ranks):
+            A = bf16(randn(seed + 100 + 20 * i + 2 * s, (r, K), 1.0 / np.sqrt(K)))
+            B = bf16(randn(seed + 101 + 20 * i + 2 * s, (N, r), 0.01))
+            lo.append((A, B, scales[s]))
         loras.append(lo)
     ws = []
     for (codes, sc, bi), lo in zip(packs, loras):
-        qw = m.QWeight.quantized(ctx, codes, sc, bi, 4)
+        qw = m.QWeight.quantized(ctx, codes, sc, bi, bits)
         for s, (A, B, _) in enumerate(lo):
             qw.bind_lora(s, A, B)
         ws.append(qw)
@@ -638,13 +638,16 @@ def test_config2_ffn_full_size(ctx, orc):
     h = empty_bf16(M, F)
     sync()
     ctx.reset_engagement()
-    ctx.ffn(ws[0], ws[1], ws[2], xd, y, M, CFG2_SCALES, h=h)
+    ctx.ffn(ws[0], ws[1], ws[2], xd, y, M, scales, h=h)
     sync()
     eng = ctx.engagement()
     auto = route_is_auto(ctx)
-    assert eng["gemm_q4"] == 3 and eng["lora_proj"] == 3 and eng["lora_xa"] == 2
+    live = sum(r for r, s in zip(ranks, scales) if s != 0.0)
+    assert eng["gemm_q%d" % bits] == 3 and eng["lora_proj"] == 3 and eng["lora_xa"] == 2
     assert eng["gemm_fast"] == (3 if auto else 0) and eng["gemm_split"] == 0
     assert eng["gemm_paired"] == (1 if auto else 0)
+    # the live stack the tails walk: every live rank, counted in the FLOP
+    assert eng["gemm_flops"] == 3 * 2 * M * H * F + 3 * 2 * M * live * (H + F)
     rows = _cfg2_rows(M)
     assert len(rows) == 51 and rows[-1] == M - 1
     yh, hh = from_dev(y)[rows], from_dev(h)[rows]
@@ -652,20 +655,85 @@ def test_config2_ffn_full_size(ctx, orc):
 
     def qp(inp, i):
         codes, sc, bi = packs[i]
-        return orc.qproj_packed(np.ascontiguousarray(inp), codes, sc, bi, 4, loras[i])
+        return orc.qproj_packed(np.ascontiguousarray(inp), codes, sc, bi, bits, loras[i])
 
     g = qp(xs, 0)
     u = qp(xs, 1)
     h_ref = orc.swiglu(orc.f32_to_bf16(g), orc.f32_to_bf16(u))
     rel_h = orc.rel_l2(orc.bf16_to_f32(hh), orc.bf16_to_f32(h_ref))
     rel_y_own = _rel(orc, yh, qp(hh, 2))
-    rel_y = _rel(orc, yh, qp(h_ref, 2))
-    base = orc.qproj_packed(xs, *packs[0], 4)
+    # the f32 chain: SiLU(g) * u and w2 (dequantized, with its adapters) on it
+    # in f64, nothing rounded to bf16
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    h32 = g64 / (1.0 + np.exp(-g64)) * u64
+    w2 = orc.dequant(*packs[2], bits).astype(np.float64)
+    y32 = h32 @ w2.T
+    for A, B, s in loras[2]:
+        if s != 0.0:
+            y32 += np.float64(np.float32(s)) * ((h32 @ orc.bf16_to_f32(A).astype(np.float64).T)
+                                                @ orc.bf16_to_f32(B).astype(np.float64).T)
+    y_bf = orc.bf16_to_f32(orc.f32_to_bf16(qp(h_ref, 2)))
+    floor = orc.rel_l2(y_bf, y32)
+    bar = max(TOL, 2.0 * floor)
+    rel_y = orc.rel_l2(orc.bf16_to_f32(yh), y32)
+    base = orc.qproj_packed(xs, *packs[0], bits)
     moved = orc.rel_l2(g, base)
-    print(f"configs[1] ffn ({'auto' if auto else 'general'}): h rel-L2 {rel_h:.3e}, "
-          f"y vs w2(own h) {rel_y_own:.3e}, y vs oracle chain {rel_y:.3e}, "
-          f"adapters move w1 by {moved:.3e}", flush=True)
-    assert rel_h <= TOL and rel_y_own <= TOL and rel_y <= np.sqrt(2.0) * TOL
+    print(f"{label} ffn ({'auto' if auto else 'general'}): h rel-L2 {rel_h:.3e}, "
+          f"y vs w2(own h) {rel_y_own:.3e}, y vs f32 chain {rel_y:.3e} (bf16 chain "
+          f"{floor:.3e}, bar {bar:.3e}), adapters move w1 by {moved:.3e}", flush=True)
+    assert rel_h <= TOL and rel_y_own <= TOL and rel_y <= bar
     assert moved > 10 * TOL
     for w in ws:
         w.close()
+
+
+def test_config2_ffn_full_size(ctx, orc):
+    """BASELINE configs[1] exactly: w4g64, the eight slots {4, 8, 16, 16, 32,
+    32, 64, 128} at strengths {1, .5, 0, -.3, .8, 0, 1.2, .25} on all three
+    weights (252 live ranks: an 8-chunk tail)."""
+    _ffn_full_size(ctx, orc, 4, CFG2_RANKS, CFG2_SCALES, 2000, "configs[1]")
+
+
+def test_config5_ffn_w8_full_size(ctx, orc):
+    """BASELINE configs[4]'s arithmetic on one block's FFN: w8g64 packs with
+    eight rank-64 slots at strengths uniform in [-1, 1.5] (all live: 512
+    ranks, a 16-chunk tail) on all three weights, through the w8 paired and
+    unsplit kernels."""
+    _ffn_full_size(ctx, orc, 8, CFG5_RANKS, CFG5_SCALES, 5000, "configs[4]")
+
+
+def test_config5_projection_w8_full_size(ctx, orc):
+    """One w8 3840 x 3840 projection over 4352 rows with configs[4]'s eight
+    rank-64 slots (255 tiles: the unsplit fast kernel, a 16-chunk tail),
+    against the oracle on a row sample over all 17 M tiles; all strengths 0
+    gives the unadapted bits."""
+    M, N, K = 4352, 3840, 3840
+    x = bf16(randn(5101, (M, K)))
+    codes, sc, bi = orc.quantize(randn(5102, (N, K), 0.02), 8)
+    qw = m.QWeight.quantized(ctx, codes, sc, bi, 8)
+    plain = m.QWeight.quantized(ctx, codes, sc, bi, 8)
+    loras = []
+    for s, r in enumerate(CFG5_RANKS):
+        A = bf16(randn(5110 + 2 * s, (r, K), 1.0 / np.sqrt(K)))
+        B = bf16(randn(5111 + 2 * s, (N, r), 0.01))
+        qw.bind_lora(s, A, B)
+        loras.append((A, B, CFG5_SCALES[s]))
+    xd = to_dev(x)
+    ctx.reset_engagement()
+    y = _run(ctx, qw, xd, M, CFG5_SCALES)
+    eng = ctx.engagement()
+    auto = route_is_auto(ctx)
+    assert eng["gemm_q8"] == 1 and eng["lora_proj"] == 1 and eng["lora_xa"] == 1
+    assert eng["gemm_fast"] == (1 if auto else 0) and eng["gemm_split"] == 0
+    assert eng["gemm_flops"] == 2 * M * N * K + 2 * M * 512 * (K + N)
+    rows = _cfg2_rows(M)
+    ref = orc.qproj_packed(np.ascontiguousarray(x[rows]), codes, sc, bi, 8, loras)
+    rel = _rel(orc, np.ascontiguousarray(y[rows]), ref)
+    moved = orc.rel_l2(ref, orc.qproj_packed(np.ascontiguousarray(x[rows]), codes, sc, bi, 8))
+    print(f"configs[4] w8 projection ({'auto' if auto else 'general'}): rel-L2 {rel:.3e}, "
+          f"adapters move it by {moved:.3e}", flush=True)
+    assert rel <= TOL and moved > 10 * TOL
+    y0 = _run(ctx, qw, xd, M, [0.0] * 8)
+    assert np.array_equal(y0, _run(ctx, plain, xd, M))
+    qw.close()
+    plain.close()
