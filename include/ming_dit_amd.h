@@ -250,6 +250,23 @@ int ming_qk_norm_rope(ming_ctx* ctx, uint16_t* x, int64_t ld, int q_col,
                       const uint16_t* wq, const uint16_t* wk,
                       const float* cos_t, const float* sin_t, float eps);
 
+/* The LLM encoder's qk-norm + RoPE, LlmOps::qk_norm_rope (ming-ops.h:118-122,
+ * ming-ops.cc:281-302; kernel ming_llm.metal:100-178), in place on the fused
+ * token-major qkv rows [rows][row_stride] bf16: heads [0, n_q) are queries
+ * from column 0, heads [n_q, n_q + n_k) keys right after them (128 wide each;
+ * n_k may differ from n_q); the value columns past them are not touched.
+ * With both q_w and k_w [128] given, each head is RMS-normalized (f32
+ * statistics, eps) and scaled by its weight first; with either one NULL there
+ * is no norm. rot_half is the rotate-half width: 64 rotates each pair
+ * (j, j + 64) of the whole head, 32 the pairs (j, j + 32) of dims 0..63 and
+ * leaves 64..127, 0 rotates nothing; cos_t / sin_t are f32 [rows][rot_half]
+ * (angle j of row r; unused at 0). One bf16 rounding per element.
+ * row_stride a multiple of 8 elements; pointers 16-byte aligned. */
+int ming_llm_qk_norm_rope(ming_ctx* ctx, uint16_t* qkv, const uint16_t* q_w,
+                          const uint16_t* k_w, const float* cos_t, const float* sin_t,
+                          int rows, int64_t row_stride, int n_q, int n_k, int rot_half,
+                          float eps);
+
 /* Dense bidirectional attention (run_attn, ming-dit.cc:1905-2039, with the
  * head-major transposes around it, 2085-2092): for every head h,
  *   out[:, 128h + d] = softmax(scale * Q_h K_h^T) V_h,

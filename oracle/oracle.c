@@ -25,6 +25,9 @@
  *   rmsnorm ......... numpy restatement + invariants (scale invariance).
  *   rope ............ rotation-by-angle closed form, norm preservation,
  *                     position 0 = identity, pair/axis assignment.
+ *   rotate-half ..... the complex rotation of the split halves (numpy
+ *                     complex128), rot_half 0 = identity / the per-head
+ *                     RMSNorm, pass-through dims, zero angle = no rotation.
  *   attention ....... numpy softmax reference, one-key and uniform cases.
  */
 #include <math.h>
@@ -567,6 +570,58 @@ or_qk_norm_rope(uint16_t* x, int ld, int q_col, int k_col, int rows,
                 table_row0);
   or_rope_apply(x, ld, k_col, rows, n_heads, head_dim, cos_t, sin_t,
                 table_row0);
+}
+
+/* The LLM encoder's fused qk-norm + rotate-half RoPE, LlmOps::qk_norm_rope
+ * (ming-ops.h:118-122, ming-ops.cc:281-302) as its kernel defines it
+ * (ming_llm.metal:100-178). In place on [rows][row_stride] bf16: heads
+ * [0, n_q) are queries from column 0, heads [n_q, n_q + n_k) keys right after
+ * them, 128 wide each; columns past them (the values) are not touched.
+ * With both weights given (ming-ops.cc:287), each head is RMS-normalized (f32
+ * statistics, eps) and scaled as x * (inv * w), w = q_w or k_w [128]; then
+ * the rotate-half rotation of half-width rot_half by the row's angles,
+ * cos/sin [rows][rot_half] f32:
+ *   32: pairs (j, j + 32) for j < 32, dims 64..127 pass through;
+ *   64: pairs (j, j + 64) for j < 64, the whole head;
+ *    0: no rotation;
+ * (x_j, x_{j+R}) -> (x_j c_j - x_{j+R} s_j, x_{j+R} c_j + x_j s_j) in f32,
+ * and each element is rounded to bf16 once at the end. Returns -1 for
+ * another rot_half. */
+OR_EXPORT int
+or_llm_qk_norm_rope(uint16_t* qkv, int row_stride, const uint16_t* q_w,
+                    const uint16_t* k_w, const float* cos_t,
+                    const float* sin_t, int rows, int n_q, int n_k,
+                    int rot_half, float eps)
+{
+  if (rot_half != 0 && rot_half != 32 && rot_half != 64) { return -1; }
+  const int norm = q_w != NULL && k_w != NULL;
+  float v[128];
+  for (int r = 0; r < rows; ++r) {
+    for (int h = 0; h < n_q + n_k; ++h) {
+      uint16_t* p = qkv + (size_t)r * row_stride + (size_t)h * 128;
+      for (int d = 0; d < 128; ++d) { v[d] = or_bf16_to_f32(p[d]); }
+      if (norm) {
+        double ss = 0.0;
+        for (int d = 0; d < 128; ++d) { ss += (double)v[d] * (double)v[d]; }
+        const float inv = 1.0f / sqrtf((float)(ss / 128.0) + eps);
+        const uint16_t* w = h < n_q ? q_w : k_w;
+        for (int d = 0; d < 128; ++d) {
+          v[d] = v[d] * (inv * or_bf16_to_f32(w[d]));
+        }
+      }
+      if (rot_half > 0) {
+        const float* c = cos_t + (size_t)r * rot_half;
+        const float* s = sin_t + (size_t)r * rot_half;
+        for (int j = 0; j < rot_half; ++j) {
+          const float a = v[j], b = v[j + rot_half];
+          v[j] = a * c[j] - b * s[j];
+          v[j + rot_half] = b * c[j] + a * s[j];
+        }
+      }
+      for (int d = 0; d < 128; ++d) { p[d] = or_bf16_rne(v[d]); }
+    }
+  }
+  return 0;
 }
 
 /* ---- sequence layout, schedule, timestep ---------------------------------- */

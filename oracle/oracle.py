@@ -76,6 +76,11 @@ def lib():
     L.or_qk_norm_rope.argtypes = [_u16p, C.c_int, C.c_int, C.c_int, C.c_int,
                                   C.c_int, C.c_int, _u16p, _u16p, _f32p,
                                   _f32p, C.c_int, C.c_float]
+    # the weights and tables are optional (NULL): passed as raw addresses
+    L.or_llm_qk_norm_rope.argtypes = [_u16p, C.c_int, C.c_void_p, C.c_void_p,
+                                      C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                      C.c_int, C.c_int, C.c_float]
+    L.or_llm_qk_norm_rope.restype = C.c_int
     L.or_build_layout.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                   C.c_void_p, C.c_void_p, C.c_void_p, _i32p]
     L.or_build_layout.restype = C.c_int
@@ -254,6 +259,35 @@ def qk_norm_rope(x_bf16, q_col, k_col, n_heads, head_dim, wq, wk, cos_t,
                           np.ascontiguousarray(cos_t, np.float32),
                           np.ascontiguousarray(sin_t, np.float32), table_row0,
                           eps)
+    return x
+
+
+def llm_qk_norm_rope(qkv_bf16, q_w, k_w, cos_t, sin_t, n_q, n_k, rot_half,
+                     eps=1e-5) -> np.ndarray:
+    """LlmOps::qk_norm_rope (ming-ops.h:118-122): heads [0, n_q) queries from
+    column 0, then n_k keys; norm only when both weights are given; rotate-half
+    of width rot_half (0, 32, 64) by cos/sin [rows][rot_half]."""
+    x = np.array(qkv_bf16, np.uint16, copy=True, order="C")
+    rows, ld = x.shape
+    norm = q_w is not None and k_w is not None
+    qw = np.ascontiguousarray(q_w, np.uint16) if norm else None
+    kw = np.ascontiguousarray(k_w, np.uint16) if norm else None
+    c = np.ascontiguousarray(cos_t, np.float32) if rot_half else None
+    s = np.ascontiguousarray(sin_t, np.float32) if rot_half else None
+    if rot_half not in (0, 32, 64):
+        raise ValueError("rot_half must be 0, 32 or 64")
+    if n_q < 0 or n_k < 0 or (n_q + n_k) * 128 > ld:
+        raise ValueError("heads past the row")
+    if rot_half and (c.shape != (rows, rot_half) or s.shape != (rows, rot_half)):
+        raise ValueError("tables must be [rows][rot_half]")
+
+    def addr(a):
+        return None if a is None else a.ctypes.data
+
+    rc = lib().or_llm_qk_norm_rope(x, ld, addr(qw), addr(kw), addr(c), addr(s), rows,
+                                   n_q, n_k, rot_half, eps)
+    if rc != 0:
+        raise ValueError("rot_half must be 0, 32 or 64")
     return x
 
 

@@ -103,3 +103,80 @@ def test_qk_norm_rope_parity(ctx, orc, rows, n_heads, ld_extra):
     assert orc.rel_l2(f32(got), f32(want)) <= TOL
     # untouched columns past q and k
     assert np.array_equal(got[:, 2 * n_heads * Hd:], x[:, 2 * n_heads * Hd:])
+
+
+def _llm_tables(rows, R, theta=10000.0):
+    """1-D positions 0..rows-1 at R frequencies theta^(-j/R) (the encoder's
+    plain rotary), f64 angles stored f32 [rows][R]."""
+    inv = theta ** (-np.arange(R, dtype=np.float64) / R)
+    ang = np.arange(rows, dtype=np.float64)[:, None] * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+@pytest.mark.parametrize("rows,n_q,n_k,n_v,rot_half,norm", [
+    (300, 16, 4, 4, 64, True),        # grouped keys, the whole head rotated
+    (4352, 30, 30, 30, 64, True),     # the DiT's head count at 1024^2
+    (257, 14, 2, 2, 32, True),        # partial rotary: dims 64..127 pass through
+    (100, 8, 8, 0, 0, True),          # norm only
+    (100, 8, 2, 2, 64, False),        # rotation only
+    (70000, 1, 1, 1, 32, True),       # more rows than the grid's y extent
+])
+def test_llm_qk_norm_rope_parity(ctx, orc, rows, n_q, n_k, n_v, rot_half, norm):
+    """LlmOps::qk_norm_rope (ming-ops.h:118-122; ming_llm.metal:100-178)
+    through ming_llm_qk_norm_rope against the oracle: q heads then k heads
+    from column 0 of the fused rows, value columns untouched, rotate-half of
+    width 64 / 32 / 0, norm with both weights or none."""
+    print(f"case llm_qk_norm_rope rows={rows} nq={n_q} nk={n_k} rot={rot_half} "
+          f"norm={norm}", flush=True)
+    import torch
+    stride = (n_q + n_k + n_v) * 128 + 8
+    x = bf16(randn(900 + rows, (rows, stride)))
+    qw = bf16(1.0 + randn(901, (128,), 0.2)) if norm else None
+    kw = bf16(0.7 + randn(902, (128,), 0.2)) if norm else None
+    c = s = None
+    if rot_half:
+        c, s = _llm_tables(rows, rot_half)
+    xd = to_dev(x)
+    dev = {k: (None if v is None else (to_dev(v) if v.dtype == np.uint16 else
+                                        torch.from_numpy(v).cuda()))
+           for k, v in (("qw", qw), ("kw", kw), ("c", c), ("s", s))}
+    ctx.reset_engagement()
+    sync()
+    ctx.llm_qk_norm_rope(xd, dev["qw"], dev["kw"], dev["c"], dev["s"], rows, stride,
+                         n_q, n_k, rot_half, 1e-6)
+    sync()
+    assert ctx.engagement()["qk_norm_rope"] == 1
+    got = from_dev(xd)
+    want = orc.llm_qk_norm_rope(x, qw, kw, c, s, n_q, n_k, rot_half, 1e-6)
+    nh = (n_q + n_k) * 128
+    assert np.array_equal(got[:, nh:], x[:, nh:])           # the values and the tail
+    u = _ulps(got[:, :nh], want[:, :nh])
+    if rot_half == 0:
+        assert u.max() <= 1 and (u > 0).mean() < 0.01
+    else:
+        # a one-ulp difference in a normalized input moves a rotated output by
+        # up to an ulp of its pair's magnitude: bound each element by 2 bf16
+        # ulps of the pair norm the rotation preserves
+        R = rot_half
+        g = f32(got[:, :nh]).reshape(rows, n_q + n_k, 128).astype(np.float64)
+        w = f32(want[:, :nh]).reshape(rows, n_q + n_k, 128).astype(np.float64)
+        pn = np.sqrt(w[..., :R] ** 2 + w[..., R:2 * R] ** 2)
+        pn = np.concatenate([pn, pn], axis=-1)
+        assert np.all(np.abs(g[..., :2 * R] - w[..., :2 * R]) <= 2.0 ** -6 * pn + 1e-30)
+        assert (u > 0).mean() < 0.02
+        if R == 32:
+            assert _ulps(got[:, :nh].reshape(rows, -1, 128)[..., 64:],
+                         want[:, :nh].reshape(rows, -1, 128)[..., 64:]).max() <= 1
+    assert orc.rel_l2(f32(got[:, :nh]), f32(want[:, :nh])) <= TOL
+
+
+def test_llm_qk_norm_rope_refusals(ctx):
+    import ming_dit_amd as m
+    x = empty_bf16(4, 3 * 128)
+    c = empty_bf16(4, 128)           # 4 x 64 f32 worth of bytes
+    with pytest.raises(m.MingError):  # rot_half 16 is no mode
+        ctx.llm_qk_norm_rope(x, None, None, c, c, 4, 3 * 128, 1, 1, 16, 1e-6)
+    with pytest.raises(m.MingError):  # heads past the row
+        ctx.llm_qk_norm_rope(x, None, None, c, c, 4, 3 * 128, 2, 2, 64, 1e-6)
+    with pytest.raises(m.MingError):  # a rotation without its tables
+        ctx.llm_qk_norm_rope(x, None, None, None, None, 4, 3 * 128, 1, 1, 64, 1e-6)

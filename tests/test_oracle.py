@@ -365,6 +365,65 @@ def test_qk_norm_rope_is_norm_then_rotation(orc):
     assert np.array_equal(y, want)
 
 
+def _angle_tables(rows, R, seed):
+    ang = randn(seed, (rows, R)).astype(np.float64) * 3.0
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+@pytest.mark.parametrize("rot_half", [32, 64])
+def test_llm_qk_norm_rope_is_rotate_half(orc, rot_half):
+    """LlmOps::qk_norm_rope (ming_llm.metal:100-178): per-head RMSNorm with
+    the q weight on heads [0, n_q) and the k weight on the next n_k, then the
+    rotation of the split halves (x_j, x_{j+R}) as one complex number times
+    e^{i angle_j}, rounded once; checked against numpy complex128 on the
+    normalized values, the earlier-pinned per-head RMSNorm, and the identities
+    the definition fixes (rot_half 0, zero angles, the pass-through dims, the
+    value columns)."""
+    rows, nq, nk, R = 7, 3, 2, rot_half
+    nh = nq + nk
+    ld = (nh + 2) * 128 + 8                      # value heads after, a ragged tail
+    x = bf16(randn(80, (rows, ld)))
+    qw = bf16(1.0 + randn(81, (128,), 0.2))
+    kw = bf16(0.5 + randn(82, (128,), 0.2))
+    c, s = _angle_tables(rows, R, 83 + R)
+    y = orc.llm_qk_norm_rope(x, qw, kw, c, s, nq, nk, R)
+    assert np.array_equal(y[:, nh * 128:], x[:, nh * 128:])
+    # no rotation, no weights: the identity
+    assert np.array_equal(orc.llm_qk_norm_rope(x, None, None, None, None, nq, nk, 0), x)
+    # normalization alone is the per-head RMSNorm, q weight then k weight
+    # (within one rounding of its product order: x * (inv * w) here)
+    n0 = orc.llm_qk_norm_rope(x, qw, kw, None, None, nq, nk, 0)
+    heads = x[:, :nh * 128].reshape(rows, nh, 128)
+    want0 = np.concatenate(
+        [orc.rmsnorm(np.ascontiguousarray(heads[:, :nq]).reshape(-1, 128), qw).reshape(rows, nq, 128),
+         orc.rmsnorm(np.ascontiguousarray(heads[:, nq:]).reshape(-1, 128), kw).reshape(rows, nk, 128)],
+        axis=1)
+    u = _ulps(n0[:, :nh * 128].reshape(rows, nh, 128), want0)
+    assert u.max() <= 1 and (u > 0).mean() < 0.01
+    # zero angles: the normalized heads unchanged, bit for bit
+    one, zero = np.ones((rows, R), np.float32), np.zeros((rows, R), np.float32)
+    assert np.array_equal(orc.llm_qk_norm_rope(x, qw, kw, one, zero, nq, nk, R), n0)
+    # the rotation of the split halves, against complex128 on the normalized values
+    v = f32(heads).astype(np.float64)
+    inv = 1.0 / np.sqrt((v * v).mean(-1, keepdims=True) + 1e-5)
+    w = np.concatenate([np.repeat(f32(qw)[None], nq, 0), np.repeat(f32(kw)[None], nk, 0)])
+    xn = v * inv * w[None].astype(np.float64)
+    z = xn[..., :R] + 1j * xn[..., R:2 * R]
+    want = z * (c.astype(np.float64) + 1j * s.astype(np.float64))[:, None, :]
+    yh = f32(y[:, :nh * 128].reshape(rows, nh, 128)).astype(np.float64)
+    got = yh[..., :R] + 1j * yh[..., R:2 * R]
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(z) + 1e-30)
+    assert np.allclose(np.abs(got), np.abs(z), rtol=1e-2)
+    # half-width 32 leaves dims 64..127 as the norm left them
+    if R == 32:
+        assert np.array_equal(y[:, :nh * 128].reshape(rows, nh, 128)[..., 64:],
+                              n0[:, :nh * 128].reshape(rows, nh, 128)[..., 64:])
+    if R == 64:      # the DiT's interleaved-pair rotation is another function
+        assert not np.array_equal(y, orc.rope_apply(n0, 0, nh, 128, c, s))
+    with pytest.raises(ValueError):
+        orc.llm_qk_norm_rope(x, qw, kw, c, s, nq, nk, 16)
+
+
 # ---- block glue ------------------------------------------------------------------------------
 def test_attention_against_numpy(orc):
     rows, H, D = 33, 2, 128

@@ -193,6 +193,12 @@ hipError_t launch_norm_residual_norm(const uint16_t* sub, long long lds, const u
 hipError_t launch_k_norm_rope(uint16_t* x, long long ld, int k_col, int rows, int n_heads,
                               const uint16_t* wk, const float* cos_t, const float* sin_t,
                               float eps, hipStream_t s);
+// LlmOps::qk_norm_rope: heads [0, nq) then nk from column 0, norm when both
+// weights are given, rotate-half of half-width rot_half (0, 32, 64) by
+// tables [rows][rot_half].
+hipError_t launch_llm_qk_norm_rope(uint16_t* x, long long ld, int rows, int nq, int nk,
+                                   const uint16_t* wq, const uint16_t* wk, const float* cos_t,
+                                   const float* sin_t, int rot_half, float eps, hipStream_t s);
 hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
                                int k_col, int rows, int n_heads,
                                const uint16_t* wq, const uint16_t* wk,

@@ -320,6 +320,108 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   }
 }
 
+// The LLM encoder's fused qk-norm + rotate-half RoPE (LlmOps::qk_norm_rope,
+// ming-ops.h:118-122; ming_llm.metal:100-178), in place: heads [0, nq) are
+// queries from column 0, heads [nq, nq + nk) keys right after them, 128 wide.
+// One 16-lane group per (row, head), each lane 8 consecutive dims, as in
+// qk_norm_rope_kernel. With NORM, each head is RMS-normalized and scaled as
+// x * (inv * w). ROT is the rotation's half-width R: element j pairs with
+// j + R, which sits R/8 lanes away (lane distance 8 for R = 64, 4 for
+// R = 32), so each lane takes its partner's 8 raw values with four
+// cross-lane moves, normalizes them itself with the partner's weights (the
+// same operations the partner applies), and computes its own side:
+// x_j c_j - x_{j+R} s_j on the low half, x_{j+R} c_j + x_j s_j on the high.
+// R = 32 leaves dims 64..127 unrotated; R = 0 rotates nothing. One bf16
+// rounding per element.
+template <int ROT, bool NORM>
+__global__ __launch_bounds__(256) void llm_qk_norm_rope_kernel(
+    uint16_t* __restrict__ x, long long ld, int rows, int nq, int nk,
+    const uint16_t* __restrict__ wq, const uint16_t* __restrict__ wk,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, float eps) {
+  constexpr int PX = ROT == 64 ? 8 : 4;
+  const int tid = threadIdx.x, sub = tid & 15;
+  const int hh0 = (int)blockIdx.x * 16 + (tid >> 4);
+  const bool live = hh0 < nq + nk;
+  const int hh = live ? hh0 : 0;
+  const bool rotated = ROT == 64 || (ROT == 32 && sub < 8);
+  const bool low = ROT == 64 ? sub < 8 : (sub & 4) == 0;
+  constexpr int RM = ROT == 0 ? 1 : ROT;
+  const int j0 = (8 * sub) % RM;       // this lane's first angle index
+  float w[8], wp[8];
+  if (NORM) {
+    const uint16_t* wb = hh < nq ? wq : wk;
+    const uint4 a = *reinterpret_cast<const uint4*>(wb + 8 * sub);
+    const uint4 b = *reinterpret_cast<const uint4*>(wb + 8 * (sub ^ PX));
+    const uint32_t ua[4] = {a.x, a.y, a.z, a.w}, ub[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w[2 * e] = bf16_lo(ua[e]);
+      w[2 * e + 1] = bf16_hi(ua[e]);
+      wp[2 * e] = bf16_lo(ub[e]);
+      wp[2 * e + 1] = bf16_hi(ub[e]);
+    }
+  }
+  for (int row = (int)blockIdx.y; row < rows; row += (int)gridDim.y) {
+    uint16_t* p = x + (long long)row * ld + hh * 128 + 8 * sub;
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    float inv = 1.0f;
+    if (NORM) {
+      float ss = head_ss8(v);
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      inv = head_rms_inv(ss, eps);
+    }
+    const uint32_t uv[4] = {v.x, v.y, v.z, v.w};
+    float a[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[2 * e] = bf16_lo(uv[e]);
+      a[2 * e + 1] = bf16_hi(uv[e]);
+    }
+    if (NORM) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = __fmul_rn(a[e], __fmul_rn(inv, w[e]));
+    }
+    if (ROT != 0) {
+      const uint32_t pu[4] = {(uint32_t)__shfl_xor((int)v.x, PX, 64),
+                              (uint32_t)__shfl_xor((int)v.y, PX, 64),
+                              (uint32_t)__shfl_xor((int)v.z, PX, 64),
+                              (uint32_t)__shfl_xor((int)v.w, PX, 64)};
+      if (rotated) {
+        float b[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          b[2 * e] = bf16_lo(pu[e]);
+          b[2 * e + 1] = bf16_hi(pu[e]);
+        }
+        if (NORM) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) b[e] = __fmul_rn(b[e], __fmul_rn(inv, wp[e]));
+        }
+        const float* cr = cos_t + (long long)row * ROT + j0;
+        const float* sr = sin_t + (long long)row * ROT + j0;
+        const float4 c0 = *reinterpret_cast<const float4*>(cr);
+        const float4 c1 = *reinterpret_cast<const float4*>(cr + 4);
+        const float4 s0 = *reinterpret_cast<const float4*>(sr);
+        const float4 s1 = *reinterpret_cast<const float4*>(sr + 4);
+        const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a[e] = low ? __fsub_rn(__fmul_rn(a[e], c[e]), __fmul_rn(b[e], s[e]))
+                     : __fadd_rn(__fmul_rn(a[e], c[e]), __fmul_rn(b[e], s[e]));
+        }
+      }
+    }
+    uint4 o;
+    o.x = pack_bf16x2_rne(a[0], a[1]);
+    o.y = pack_bf16x2_rne(a[2], a[3]);
+    o.z = pack_bf16x2_rne(a[4], a[5]);
+    o.w = pack_bf16x2_rne(a[6], a[7]);
+    if (live) *reinterpret_cast<uint4*>(p) = o;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm_ex(int mode, const uint16_t* x, long long ldx, const uint16_t* w,
@@ -426,6 +528,28 @@ hipError_t launch_k_norm_rope(uint16_t* x, long long ld, int k_col, int rows, in
   return hipGetLastError();
 }
 
+hipError_t launch_llm_qk_norm_rope(uint16_t* x, long long ld, int rows, int nq, int nk,
+                                   const uint16_t* wq, const uint16_t* wk, const float* cos_t,
+                                   const float* sin_t, int rot_half, float eps, hipStream_t s) {
+  if (rows <= 0 || nq + nk <= 0) return hipSuccess;
+  const bool norm = wq != nullptr && wk != nullptr;
+  const dim3 grid((unsigned)((nq + nk + 15) / 16), (unsigned)(rows < 65535 ? rows : 65535));
+#define MING_LLMQK(R, N)                                                                  \
+  hipLaunchKernelGGL((llm_qk_norm_rope_kernel<R, N>), grid, dim3(256), 0, s, x, ld, rows, \
+                     nq, nk, wq, wk, cos_t, sin_t, eps)
+  if (rot_half == 64) {
+    if (norm) MING_LLMQK(64, true); else MING_LLMQK(64, false);
+  } else if (rot_half == 32) {
+    if (norm) MING_LLMQK(32, true); else MING_LLMQK(32, false);
+  } else if (rot_half == 0) {
+    if (norm) MING_LLMQK(0, true); else MING_LLMQK(0, false);
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef MING_LLMQK
+  return hipGetLastError();
+}
+
 }  // namespace ming
 
 namespace ming {
@@ -447,7 +571,13 @@ hipError_t validate_norm_kernels() {
       MING_NRN_ALL(64, 4), MING_NRN_ALL(64, 8), MING_NRN_ALL(64, 16),
 #undef MING_NRN_ALL
       reinterpret_cast<const void*>(&rope_table_kernel),
-      reinterpret_cast<const void*>(&qk_norm_rope_kernel)};
+      reinterpret_cast<const void*>(&qk_norm_rope_kernel),
+      reinterpret_cast<const void*>(&llm_qk_norm_rope_kernel<64, true>),
+      reinterpret_cast<const void*>(&llm_qk_norm_rope_kernel<64, false>),
+      reinterpret_cast<const void*>(&llm_qk_norm_rope_kernel<32, true>),
+      reinterpret_cast<const void*>(&llm_qk_norm_rope_kernel<32, false>),
+      reinterpret_cast<const void*>(&llm_qk_norm_rope_kernel<0, true>),
+      reinterpret_cast<const void*>(&llm_qk_norm_rope_kernel<0, false>)};
   for (const void* f : fns) {
     const hipError_t e = hipFuncGetAttributes(&fa, f);
     if (e != hipSuccess) return e;

@@ -1408,6 +1408,36 @@ int ming_qk_norm_rope(ming_ctx* c, uint16_t* x, int64_t ld, int q_col, int k_col
   return ok();
 }
 
+int ming_llm_qk_norm_rope(ming_ctx* c, uint16_t* qkv, const uint16_t* q_w,
+                          const uint16_t* k_w, const float* cos_t, const float* sin_t,
+                          int rows, int64_t row_stride, int n_q, int n_k, int rot_half,
+                          float eps) {
+  if (!c || !qkv) return fail(MING_ERR_ARG, "ming_llm_qk_norm_rope: null argument");
+  if (rot_half != 0 && rot_half != 32 && rot_half != 64)
+    return fail(MING_ERR_ARG, "ming_llm_qk_norm_rope: rot_half must be 0, 32 or 64");
+  if (rot_half != 0 && (!cos_t || !sin_t))
+    return fail(MING_ERR_ARG, "ming_llm_qk_norm_rope: a rotation needs its cos and sin tables");
+  if (rows < 0 || n_q < 0 || n_k < 0 || row_stride % 8 ||
+      (int64_t)(n_q + n_k) * 128 > row_stride)
+    return fail(MING_ERR_SHAPE, "ming_llm_qk_norm_rope: heads past the row stride");
+  const bool norm = q_w && k_w;
+  if (!aligned(qkv, 16) || (norm && (!aligned(q_w, 16) || !aligned(k_w, 16))) ||
+      (rot_half && (!aligned(cos_t, 16) || !aligned(sin_t, 16))))
+    return fail(MING_ERR_ARG, "ming_llm_qk_norm_rope: pointers must be 16-byte aligned");
+  if (rows == 0 || n_q + n_k == 0) return ok();
+  DeviceGuard g(c->device);
+  const double bytes = 4.0 * rows * (n_q + n_k) * 128 + 8.0 * rows * rot_half;
+  MING_HIP(profiled(c, kBQkRope, 0.0, bytes,
+                    [&] {
+                      return ming::launch_llm_qk_norm_rope(
+                          qkv, row_stride, rows, n_q, n_k, norm ? q_w : nullptr,
+                          norm ? k_w : nullptr, cos_t, sin_t, rot_half, eps, c->stream);
+                    }),
+           "llm_qk_norm_rope launch");
+  c->eng.qk_norm_rope += 1;
+  return ok();
+}
+
 // oh: optional fp16 copy of the output (the context's xh plane, row stride
 // n_heads * 128) for the o-projection's fast route.
 // qn: q and k arrive as raw projection outputs; k is normed + rotated in

@@ -212,6 +212,8 @@ def lib():
                             f32], i32),
         "ming_qk_norm_rope": ([vp, vp, i64, i32, i32, i32, i32, i32, vp, vp,
                                vp, vp, f32], i32),
+        "ming_llm_qk_norm_rope": ([vp, vp, vp, vp, vp, vp, i32, i64, i32, i32,
+                                   i32, f32], i32),
         "ming_ctx_set_profiling": ([vp, i32], i32),
         "ming_ctx_set_route": ([vp, i32], i32),
         "ming_qweight_fast": ([vp], i32),
@@ -411,6 +413,16 @@ class Ctx:
                                        n_heads, head_dim, _ptr(wq), _ptr(wk),
                                        _ptr(cos_t), _ptr(sin_t), eps))
 
+    def llm_qk_norm_rope(self, qkv, q_w, k_w, cos_t, sin_t, rows: int,
+                         row_stride: int, n_q: int, n_k: int, rot_half: int,
+                         eps: float):
+        """LlmOps::qk_norm_rope (ming-ops.h:118-122), its argument order:
+        q_w / k_w None for no norm, cos_t / sin_t None when rot_half is 0."""
+        def opt(t):
+            return None if t is None else _ptr(t)
+        _check(lib().ming_llm_qk_norm_rope(self.h, _ptr(qkv), opt(q_w), opt(k_w),
+                                           opt(cos_t), opt(sin_t), rows, row_stride,
+                                           n_q, n_k, rot_half, eps))
 
     def attention(self, qkv, ld: int, q_col: int, k_col: int, v_col: int,
                   out, ldo: int, rows: int, n_heads: int, scale=None,
