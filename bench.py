@@ -327,7 +327,6 @@ def time_forward(ctx, m, torch, gen, steps, warmup):
     """34-block forward at 1024^2 (4096 image + 256 caption tokens): ms per
     forward, host clock around ming_model_forward (synchronous)."""
     import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
     model = build_forward_model(ctx, m, torch, gen)
     # every forward runs all 34 blocks: the caption cache (which would serve
     # the context refiner from the previous forward) is off

@@ -80,10 +80,16 @@ typedef struct ming_engagement {
  * weight's scales and biases are exact in fp16, and a GEMV (each weight
  * streamed once, f32 dot products) for M <= 8 rows with no live adapter, as
  * the adaLN and timestep projections run at M = 1. GENERAL always takes the
- * general kernel. Both multiply fp16 activations (bf16 values carried
- * exactly below 2^16 in magnitude); a value of 2^16 or more, inf or NaN
+ * general kernel. Both multiply fp16 activations: bf16 values are carried
+ * exactly at magnitudes in [2^-17, 2^16); smaller ones are cut toward zero
+ * to fp16's subnormal step of 2^-24 (below 2^-24 they become 0; an absolute
+ * error of at most 2^-24, not reported). A value of 2^16 or more, inf or NaN
  * cannot be carried, and the next ming_ctx_synchronize (or the forward that
- * met it) returns MING_ERR_RANGE instead of results. WIDE multiplies the
+ * met it) returns MING_ERR_RANGE instead of results. The report is pending
+ * for the CONTEXT, not for the call that met it: it stays raised until the
+ * next ming_ctx_synchronize or ming_model_forward collects it, so a caller
+ * that waits for the stream some other way should call ming_ctx_synchronize
+ * after a projection whose inputs it does not control. WIDE multiplies the
  * bf16 activations themselves with each dequantized weight split into a
  * bf16 pair (hi + lo, twice the MFMA work): no range limit, for inputs that
  * the fp16 routes refuse. All compute the same function to the same bar. */
@@ -416,7 +422,10 @@ float ming_model_lora_scale(const ming_model* m, int slot);
  * rows first); out [img_tokens][patch_dim] device, the velocity before
  * negation. Synchronous: returns after the GPU finished. MING_ERR_RANGE when a
  * projection input could not be carried in fp16 on the context's route (the
- * output is then not valid; MING_ROUTE_WIDE runs such a forward). */
+ * output is then not valid; MING_ROUTE_WIDE runs such a forward). The range
+ * report is the context's: one left pending by an earlier ming_lin / ming_ffn
+ * that no ming_ctx_synchronize collected fails this forward too, so collect
+ * it before. */
 int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* cap,
                        int64_t cap_stride, int img_tokens, int cap_len, int query_rows,
                        const int32_t* pos_t, const int32_t* pos_h, const int32_t* pos_w,

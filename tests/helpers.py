@@ -87,8 +87,8 @@ def block_proj_shapes(H, F):
 def build_block(ctx, seed, H, F, adaln, bits=4, modulated=True,
                 slots=((0, 4, 1.0), (3, 16, 0.5))):
     """A random block as (oracle dict, gpu dict, BlockDesc). Weights ~ N(0, .02)
-    quantized by the oracle's packer; gains ~ 1 + N(0, .1); adaLN bias
-    ~ N(0, .1); LoRA (slot, rank, fold) bound on all seven projections. Every
+    quantized by the oracle's packer (bits 4 / 8) or dense bf16 (bits 16);
+    gains ~ 1 + N(0, .1); adaLN bias ~ N(0, .1); LoRA (slot, rank, fold) bound on all seven projections. Every
     tensor has a fixed seed of its own, so the same seed with other slots
     gives the same base block. With ctx None only the oracle dict is made
     (gp and the desc are None)."""
@@ -100,8 +100,10 @@ def build_block(ctx, seed, H, F, adaln, bits=4, modulated=True,
     for i, (name, (N, K)) in enumerate(block_proj_shapes(H, F).items()):
         pack, _ = make_weight(seed + 100 * i, N, K, bits)
         ob[name] = dict(pack, bits=bits)
-        qw = m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
-                                 pack["biases"], bits) if gpu else None
+        qw = None
+        if gpu:
+            qw = m.QWeight.dense(ctx, pack["w"]) if bits == 16 else m.QWeight.quantized(
+                ctx, pack["codes"], pack["scales"], pack["biases"], bits)
         lor = [None] * 8
         for slot, rank, fold in slots:
             A, B = make_lora(seed + 100 * i + 10 + 2 * slot, N, K, rank)
@@ -114,8 +116,8 @@ def build_block(ctx, seed, H, F, adaln, bits=4, modulated=True,
         pack, _ = make_weight(seed + 1000, 4 * H, adaln, bits)
         ob["ada"] = dict(pack, bits=bits)
         if gpu:
-            gp["ada"] = m.QWeight.quantized(ctx, pack["codes"], pack["scales"],
-                                            pack["biases"], bits)
+            gp["ada"] = m.QWeight.dense(ctx, pack["w"]) if bits == 16 else m.QWeight.quantized(
+                ctx, pack["codes"], pack["scales"], pack["biases"], bits)
         ob["ada_b"] = bf16(randn(seed + 1001, (4 * H,), 0.1))
         if gpu:
             gp["ada_b"] = to_dev(ob["ada_b"])

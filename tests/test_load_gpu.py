@@ -266,16 +266,16 @@ def test_foreign_and_wrong_shape_adapters_are_refused_and_said(ctx, files):
             assert model.lora_modules(0) == 0
             assert model.lora_skipped(0) == (0 if k == "foreign" else 1)
             if k == "foreign":
-                assert "bound NO modules" in rep
+                assert "matched zero modules" in rep
             else:
-                assert "is NOT applied" in rep and "wrong shape (1 fit)" in rep
+                assert "left unbound" in rep and "other shapes (1 fit)" in rep
             assert any(lvl == m.LOG_WARN and s == rep for lvl, s in msgs)
             ctx.reset_engagement()
             assert np.array_equal(run(model), base)
             assert ctx.engagement()["lora_proj"] == 0
             model.close()
         model = m.Model.load(ctx, files["w4"], [(files["ad"]["foreign"] + ".missing", 1.0)])
-        assert model.lora_modules(0) == 0 and "did not open" in model.lora_report(0)
+        assert model.lora_modules(0) == 0 and "could not be read" in model.lora_report(0)
         model.close()
     finally:
         m.set_log_sink(None)
@@ -337,7 +337,7 @@ def test_caption_cache(ctx, files):
 def test_load_refuses_what_it_does_not_run(ctx, tmp_path):
     d = str(tmp_path / "learned")
     make_checkpoint(d, seed=12, cfg=config(alignment_padding_mode="learned"), shards=1)
-    with pytest.raises(m.MingError, match="zero_masked checkpoints only"):
+    with pytest.raises(m.MingError, match="learned caption padding"):
         m.Model.load(ctx, d)
     d = str(tmp_path / "short")
     make_checkpoint(d, seed=12, cfg=CFG, shards=1, drop=("layers.1.ffn_norm2.weight",))

@@ -209,6 +209,44 @@ def test_block_fault_in_the_norm_copy_and_wide_block(ctx, orc):
     assert orc.rel_l2(f32(got), f32(ref)) <= 1e-2 and upd <= 2e-2
 
 
+def test_dense_block_writes_no_fault(ctx, orc):
+    """A block of dense projections multiplies bf16 activations: the fp16
+    copies the block driver still writes are never read, so the same 1e5
+    pre-norm gain raises no range fault on the auto route, and the block
+    meets the oracle's block bars."""
+    H, NH, F, ADA, rows = 256, 2, 512, 64, 130
+    ob, gp, desc = build_block(ctx, 321, H, F, ADA, 16, False)
+    big = bf16(np.full(H, 1.0e5, np.float32))
+    ob["an1"] = big
+    gp["an1"].copy_(to_dev(big))
+    x = bf16(randn(46, (rows, H)))
+    c, s = orc.rope_table(*grid_positions(rows))
+    cd, sd = to_dev(np.ascontiguousarray(c)), to_dev(np.ascontiguousarray(s))
+    scales = (1.0, 0, 0, -0.5)
+    xd = to_dev(x)
+    ctx.set_route("auto")
+    ctx.reset_engagement()
+    sync()
+    ctx.block_forward(desc, m.BlockDims(H, NH, F, ADA, 1e-5), xd, rows, cd, sd, None, scales)
+    ctx.synchronize()                      # raises MingError on a range fault
+    sync()
+    eng = ctx.engagement()
+    assert eng["range_faults"] == 0 and eng["gemm_dense"] == 7
+    got = from_dev(xd)
+    ref = orc.block_forward(x, ob, NH, c, s, None, scales)
+    upd = orc.rel_l2(f32(got) - f32(x), f32(ref) - f32(x))
+    print(f"dense block with a 1e5 gain: output {orc.rel_l2(f32(got), f32(ref)):.3e}, "
+          f"update {upd:.3e}")
+    assert orc.rel_l2(f32(got), f32(ref)) <= 1e-2 and upd <= 2e-2
+    # the same block quantized still refuses (the copies feed fp16 routes)
+    obq, gpq, descq = build_block(ctx, 321, H, F, ADA, 4, False)
+    gpq["an1"].copy_(to_dev(big))
+    xd = to_dev(x)
+    sync()
+    ctx.block_forward(descq, m.BlockDims(H, NH, F, ADA, 1e-5), xd, rows, cd, sd, None, scales)
+    _refused(ctx)
+
+
 def test_model_forward_fault_and_wide_forward(ctx, orc):
     """The forward itself returns MING_ERR_RANGE; the caption-cache entry that
     forward filled never becomes valid; on the wide route the forward runs,

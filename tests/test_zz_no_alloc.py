@@ -3,7 +3,8 @@ scratch is the device's static array) against ming_lin, through the C-ABI:
 the same bits on consecutive calls that shrink, on the fast route's unsplit
 and split kernels and the general route; no device memory taken by it; and
 its refusals (a call beyond the array, a weight whose adapter stacks are not
-built) before anything runs. It has no counterpart in the reference."""
+built) before anything runs. The auto, general and wide routes, and a dense
+weight on a few tiles (the split-K bf16 GEMM) are each held to ming_lin. It has no counterpart in the reference."""
 import numpy as np
 import pytest
 
@@ -16,7 +17,10 @@ pytestmark = pytest.mark.gpu
 
 def _weight(ctx, seed, N, K, bits, ranks):
     pack, _ = make_weight(seed, N, K, bits)
-    qw = m.QWeight.quantized(ctx, pack["codes"], pack["scales"], pack["biases"], bits)
+    if bits == 16:
+        qw = m.QWeight.dense(ctx, pack["w"])
+    else:
+        qw = m.QWeight.quantized(ctx, pack["codes"], pack["scales"], pack["biases"], bits)
     for s, r in enumerate(ranks):
         A, B = make_lora(seed + 10 + 2 * s, N, K, r)
         qw.bind_lora(s, A, B)
@@ -43,18 +47,24 @@ def test_noalloc_matches_ming_lin_on_calls_that_shrink(ctx):
         (4352, 10240, 3840, 4, CFG2_RANKS, CFG2_SCALES),       # 680 tiles, 8-chunk tail
         (300, 512, 640, 8, (16, 64), (0.7, -0.4)),             # ragged, two slots
         (256, 3840, 3840, 4, CFG2_RANKS, CFG2_SCALES),         # 15 tiles: split K
+        # dense, no adapter, 15 tiles: the split-K bf16 GEMM (its partials
+        # carved from the array)
+        (256, 3840, 2560, 16, (), ()),
     ]
     weights = [_weight(ctx, 900 + 7 * i, N, K, b, r) for i, (M, N, K, b, r, s) in enumerate(cases)]
     xs = [to_dev(bf16(randn(950 + i, (M, K)))) for i, (M, N, K, b, r, s) in enumerate(cases)]
-    for route in ("auto", "general"):
+    for route in ("auto", "general", "wide"):
         ctx.set_route(route)
         for (M, N, K, bits, ranks, sc), qw, x in zip(cases, weights, xs):
             print(f"case noalloc {route} M={M} N={N} K={K} w{bits}", flush=True)
             ctx.reset_engagement()
             y0, y1 = _both(ctx, qw, x, M, sc)
             eng = ctx.engagement()
-            assert eng["lora_proj"] == 2 and eng["lora_xa"] == 2
-            if route == "auto":
+            adapted = 2 if ranks else 0
+            assert eng["lora_proj"] == adapted and eng["lora_xa"] == adapted
+            if bits == 16:
+                assert eng["gemm_dense"] == 2 and eng["gemm_fast"] == 0
+            elif route == "auto":
                 # the fast route splits K below 64 tiles into about one round of
                 # the chip, at least 6 K steps a slice, when that gives 2 or more
                 tiles = ((M + 255) // 256) * ((N + 255) // 256)

@@ -57,12 +57,15 @@ __device__ __forceinline__ float silu_f(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// Two bf16 (one u32) -> two fp16 (one u32). Exact for every finite value of
-// magnitude below 2^16 (bf16's largest below it, 65280, is an fp16 value),
-// so the rounding mode of the packed conversion is moot there. A finite
-// value of 2^16 or more SATURATES to +-65504 (round toward zero): the
-// writers of fp16 copies track what they convert with range_track and report
-// it with range_report, and the host turns a report into MING_ERR_RANGE.
+// Two bf16 (one u32) -> two fp16 (one u32), rounding toward zero. Exact for
+// zero and every magnitude in [2^-17, 2^16): bf16's 8 significant bits fit
+// fp16's normals, its subnormals down to 2^-17 (a step of 2^-24), and bf16's
+// largest value below 2^16, 65280. A finite value of 2^16 or more SATURATES
+// to +-65504: the writers of fp16 copies track what they convert with
+// range_track and report it with range_report, and the host turns a report
+// into MING_ERR_RANGE. Below 2^-17 the low bits are cut to fp16's 2^-24 grid
+// and below 2^-24 the value becomes +-0; that loss is NOT tracked (at most
+// 2^-24 absolute, against activations of order 1 after the norms).
 __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t u) {
   auto h = __builtin_amdgcn_cvt_pkrtz(bf16_lo(u), bf16_hi(u));
   return __builtin_bit_cast(uint32_t, h);

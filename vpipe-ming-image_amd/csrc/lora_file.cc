@@ -149,7 +149,7 @@ int bind_slot(ming_model* m, int slot, const ming_lora_spec& spec) {
   ming::st::Set file;
   std::string err;
   if (!file.open_file(path, &err)) {
-    m->lora_report[slot] = who + " did not open (" + err + "); it is NOT applied";
+    m->lora_report[slot] = who + " could not be read (" + err + "); this slot stays empty";
     ming::rt_log(MING_LOG_WARN, m->lora_report[slot]);
     return MING_OK;
   }
@@ -197,11 +197,10 @@ int bind_slot(ming_model* m, int slot, const ming_lora_spec& spec) {
     // adapter, not a weaker one (ming-dit.cc:2966-2979)
     m->lora_skipped[slot] = skipped;
     m->lora_modules[slot] = 0;
-    m->lora_report[slot] = who + " is NOT applied: " + std::to_string(skipped) +
-                           " module(s) matched by name at the wrong shape (" +
+    m->lora_report[slot] = who + " left unbound: " + std::to_string(skipped) +
+                           " of its modules have this model's names but other shapes (" +
                            std::to_string(fits.size()) +
-                           " fit) -- it was trained against a different model; the base "
-                           "model runs";
+                           " fit), so it belongs to another model; this slot stays empty";
     ming::rt_log(MING_LOG_WARN, m->lora_report[slot]);
     return rt_ok();
   }
@@ -229,8 +228,8 @@ int bind_slot(ming_model* m, int slot, const ming_lora_spec& spec) {
   if (bound == 0) {
     // loud: an adapter for another model would otherwise say nothing
     m->lora_report[slot] = who +
-                           " bound NO modules -- it is for a different model, or its names are "
-                           "in a convention this family does not map; the base model runs";
+                           " matched zero modules: none of its names is one of this model's "
+                           "projections in a known spelling; this slot stays empty";
     ming::rt_log(MING_LOG_WARN, m->lora_report[slot]);
   } else {
     char buf[160];
@@ -255,9 +254,9 @@ int ming_model_bind_loras(ming_model* m, const ming_lora_spec* loras, int n) {
     const bool named = spec.path && *spec.path;
     if (slot >= MING_MAX_LORA_SLOTS) {
       if (named)
-        ming::rt_log(MING_LOG_WARN, "ming-image DiT: only " + std::to_string(MING_MAX_LORA_SLOTS) +
-                                        " adapters run at once; '" + spec.path +
-                                        "' is NOT applied");
+        ming::rt_log(MING_LOG_WARN, "ming_model_bind_loras: slot " + std::to_string(slot) +
+                                        " is past the " + std::to_string(MING_MAX_LORA_SLOTS) +
+                                        " slots; '" + spec.path + "' is ignored");
       continue;
     }
     if (!std::isfinite(spec.scale))

@@ -114,6 +114,19 @@ int block_forward(ming_ctx* c, const ming_block_desc* b, const ming_block_dims& 
   const int H = d.hidden, F = d.ffn, NH = d.n_heads;
   const bool modulated = b->ada != nullptr;
   const float eps = d.eps;
+  // The fp16 copies this block writes (the pre-norms', attention's O, the
+  // SwiGLU's h) feed only its projections. Over dense projections (bf16
+  // activations) they are never read, so a value they cannot hold raises
+  // no range fault.
+  struct CopiesUnread {
+    ming_ctx* c;
+    bool was;
+    ~CopiesUnread() { ming::rt_set_copies_unread(c, was); }
+  };
+  bool dense = true;
+  for (const ming_qweight* q : {b->q, b->k, b->v, b->o, b->w1, b->w3, b->w2})
+    dense = dense && ming_qweight_bits(q) == 16;
+  const CopiesUnread unread{c, ming::rt_set_copies_unread(c, dense)};
   const uint16_t* g1 = b->an1;
   const uint16_t* g3 = b->fn1;
   const float* tg = nullptr;
@@ -568,7 +581,7 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
     if (pos_t[t] < 0 || pos_h[t] < 0 || pos_w[t] < 0 || pos_t[t] >= d.axes_lens[0] ||
         pos_h[t] >= d.axes_lens[1] || pos_w[t] >= d.axes_lens[2])
       return rt_fail(MING_ERR_SHAPE,
-                     "ming_model_forward: a rotary position is past the model's axes_lens");
+                     "ming_model_forward: a position lies outside the rotary table's range on its axis (axes_lens)");
   if (!std::isfinite(sigma))
     return rt_fail(MING_ERR_ARG, "ming_model_forward: sigma must be finite");
   RC(ensure_model_ws(m, JT, Q));

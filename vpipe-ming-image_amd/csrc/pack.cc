@@ -84,14 +84,14 @@ bool read_json_file(const fs::path& p, ming::json::Value* out, std::string* why)
 int read_config(const std::string& dir, ming::json::Value* t, ming_dit_config* d) {
   std::string jerr;
   if (!read_json_file(fs::path(dir) / "config.json", t, &jerr) || !t->is_obj())
-    return rt_fail(MING_ERR_ARG, "'" + dir + "': no transformer/config.json" +
+    return rt_fail(MING_ERR_ARG, "'" + dir + "': config.json is missing or not a JSON object" +
                                      (jerr.empty() ? "" : " (" + jerr + ")"));
   if (get_str(*t, "_class_name") != "DiffusionTransformer")
-    return rt_fail(MING_ERR_ARG, "transformer/config.json is not a DiffusionTransformer");
+    return rt_fail(MING_ERR_ARG, "config.json: _class_name must be DiffusionTransformer for this path");
   if (!t->get("alignment_padding_mode") || !t->get("multi_frame_output"))
     return rt_fail(MING_ERR_ARG,
-                   "transformer/config.json lacks the Ming checkpoint contract "
-                   "(alignment_padding_mode + multi_frame_output)");
+                   "config.json: both alignment_padding_mode and multi_frame_output are "
+                   "required keys of a Ming-Image DiT checkpoint, and one is absent");
   ming_dit_config c{};
   c.dim = get_int(*t, "dim", 3840);
   c.n_layers = get_int(*t, "n_layers", 30);
@@ -113,10 +113,12 @@ int read_config(const std::string& dir, ming::json::Value* t, ming_dit_config* d
   const std::string pad = get_str(*t, "alignment_padding_mode");
   c.multi_frame_output = get_bool(*t, "multi_frame_output", false) ? 1 : 0;
   if (pad != "zero_masked" && pad != "learned")
-    return rt_fail(MING_ERR_ARG, "unknown alignment_padding_mode '" + pad + "'");
+    return rt_fail(MING_ERR_ARG, "config.json: alignment_padding_mode '" + pad +
+                                     "' is neither zero_masked nor learned");
   c.zero_masked = pad == "zero_masked" ? 1 : 0;
   if (ad.size() != 3 || al.size() != 3 || c.n_heads <= 0 || c.dim % c.n_heads != 0)
-    return rt_fail(MING_ERR_ARG, "transformer/config.json has an unexpected geometry");
+    return rt_fail(MING_ERR_ARG, "config.json: axes need three dims and three lengths, and dim "
+                                 "a positive multiple of n_heads");
   for (int i = 0; i < 3; ++i) {
     c.axes_dims[i] = ad[(size_t)i];
     c.axes_lens[i] = al[(size_t)i];
@@ -135,21 +137,22 @@ int read_config(const std::string& dir, ming::json::Value* t, ming_dit_config* d
 int check_config(const ming_dit_config& d) {
   auto no = [](const std::string& m) { return rt_fail(MING_ERR_SHAPE, "ming_model_load: " + m); };
   if (d.n_heads <= 0 || d.dim <= 0 || d.dim % d.n_heads != 0)
-    return no("dim is not a whole number of heads");
-  if (d.n_kv_heads != d.n_heads) return no("n_kv_heads != n_heads (GQA) is not supported");
+    return no("the model width does not split evenly into its heads");
+  if (d.n_kv_heads != d.n_heads)
+    return no("grouped keys (n_kv_heads differing from n_heads) are outside this path");
   if (!d.zero_masked)
-    return no("alignment_padding_mode 'learned' -- this DiT runs zero_masked checkpoints only");
-  if (d.multi_frame_output) return no("multi_frame_output -- this DiT runs one frame");
-  if (!d.qk_norm) return no("qk_norm false is not supported");
+    return no("learned caption padding is outside this path (it runs zero_masked padding)");
+  if (d.multi_frame_output) return no("a multi-frame checkpoint is outside this path (one frame)");
+  if (!d.qk_norm) return no("a checkpoint without per-head q/k norms is outside this path");
   if (d.f_patch != 1 || d.patch <= 0)
-    return no("only all_f_patch_size [1] and a positive patch run here");
+    return no("the frame patch must be 1 and the spatial patch positive");
   if (d.axes_dims[0] + d.axes_dims[1] + d.axes_dims[2] != d.dim / d.n_heads)
-    return no("sum(axes_dims) != head_dim");
+    return no("the three rotary axis widths must add up to the head width");
   if (d.dim / d.n_heads != 128)
-    return no("head_dim " + std::to_string(d.dim / d.n_heads) +
-              " -- the attention here is the 128-wide kernel");
+    return no("heads of width " + std::to_string(d.dim / d.n_heads) +
+              ": the attention kernel takes 128-wide heads only");
   if (d.n_layers <= 0 || d.n_refiner_layers <= 0 || d.cap_feat_dim <= 0 || d.in_channels <= 0)
-    return no("a stack or a width in the config is not positive");
+    return no("layer counts, caption width and input channels must all be above zero");
   return MING_OK;
 }
 
@@ -170,8 +173,9 @@ int detect(ming_pack* p) {
   const ming::st::Tensor* si = p->tensors.find(p0 + "attention.to_q.scales");
   const ming::st::Tensor* ci = p->tensors.find(p0 + "attention.to_q.weight");
   if (!ci)
-    return rt_fail(MING_ERR_ARG, "'" + p0 + "attention.to_q.weight' is not in the checkpoint "
-                                 "-- not this model's transformer");
+    return rt_fail(MING_ERR_ARG, "the first block's query weight '" + p0 +
+                                 "attention.to_q.weight' is absent: the tensors are not this "
+                                 "model's transformer");
   p->quant_bits = 0;
   p->quant_group = 0;
   if (si && si->shape.size() == 2 && ci->shape.size() == 2 && si->shape[1] > 0) {

@@ -32,6 +32,9 @@ uint64_t rt_qweight_bind_gen(const ming_qweight* q);
 // After the stream has drained: MING_ERR_RANGE (counted, reason set, word
 // cleared) when an fp16 copy met a value it cannot hold since the last check.
 int rt_take_range_fault(ming_ctx* c, const char* who);
+// Marks the fp16 activation copies written from here on as unread (a block
+// whose projections are all dense); returns the previous mark.
+bool rt_set_copies_unread(ming_ctx* c, bool unread);
 
 // Fused forms the block driver uses (same bits as the public calls they
 // replace):

@@ -83,6 +83,9 @@ struct ming_ctx {
   // device word raised by any fp16 copy that could not hold its value
   // (range_report); read and cleared at synchronization points
   int* range = nullptr;
+  // set by the block driver while the block's projections are dense: the fp16
+  // copies it writes are then never read, so they raise nothing
+  bool copies_unread = false;
   int live_weights = 0;   // a context outlives every weight made on it
   // Per-launch HIP-event timing (ming_ctx_set_profiling), by bucket.
   bool profiling = false;
@@ -397,9 +400,10 @@ void* noalloc_ptr(int device) {
 
 // The range word the kernels raise: on the fp16 routes (auto, general);
 // the wide route converts nothing to fp16, and whatever fp16 copies the block
-// driver still writes there are not read.
+// driver still writes there are not read; nor are the copies a block of dense
+// projections writes (those multiply bf16 activations).
 int* range_word(const ming_ctx* c) {
-  return c->route == MING_ROUTE_WIDE ? nullptr : c->range;
+  return c->route == MING_ROUTE_WIDE || c->copies_unread ? nullptr : c->range;
 }
 
 // Reads the range word after the stream has drained: raised means some
@@ -1059,6 +1063,8 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
                     outs[1].ldg == outs[0].ldy && !outs[0].gate && !outs[0].yh && fast[0] &&
                     fast[1] && split_ks[0] == 0 && split_ks[1] == 0 &&
                     qs[0]->bits == qs[1]->bits && qs[0]->N == qs[1]->N && qs[0]->N % 8 == 0 &&
+                    outs[1].ldy % 8 == 0 && aligned(outs[1].y, 16) &&
+                    (!outs[1].yh || aligned(outs[1].yh, 16)) &&
                     qs[0]->segs.size() == 1 && qs[1]->segs.size() == 1 &&
                     qa[0].seg[0].chunks == qa[1].seg[0].chunks &&
                     qp_used[0] + qp_used[1] <= ming::kMaxGroups;
@@ -1779,6 +1785,12 @@ void rt_free(ming_ctx* c, void* dev) {
 
 void rt_note_cap_hit(ming_ctx* c) { c->eng.cap_cache_hits += 1; }
 uint64_t rt_qweight_bind_gen(const ming_qweight* q) { return q ? q->bind_gen : 0; }
+
+bool rt_set_copies_unread(ming_ctx* c, bool unread) {
+  const bool was = c->copies_unread;
+  c->copies_unread = unread;
+  return was;
+}
 
 int rt_take_range_fault(ming_ctx* c, const char* who) {
   DeviceGuard dg(c->device);
