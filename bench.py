@@ -511,6 +511,23 @@ def measured_traffic():
     return None
 
 
+TIMELINE_MD = os.path.join(ROOT, "profiles", "ffn_step_timeline_config2.md")
+
+
+def steady_pair_launch_us():
+    """The paired launch's duration in the event-free pass (its two kernels
+    back to back), from the committed rocprofv3 kernel trace of this bench's
+    default FFN command; None when absent."""
+    try:
+        with open(TIMELINE_MD) as f:
+            for line in f:
+                if line.startswith("steady_pair_launch_us:"):
+                    return float(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def mfma_ceiling(torch, seconds=2.0, variants=("f16_random", "bf16_random", "f16_zero")):
     """The sustained MFMA rate of a kernel that does nothing else (see
     vpipe-ming-image_amd/calib/mfma_ceiling.hip): per variant, launches of
@@ -699,6 +716,17 @@ def main():
                      "flop_per_launch": round(q["flops"] / q["launches"])},
         "kernels": kernels,
     }
+    steady = steady_pair_launch_us()
+    if steady and qname.startswith("qproj_pair"):
+        # the same kernel in the event-free pass that `value` is timed on,
+        # where nothing between launches lets the clock recover (read from
+        # the committed trace; the profiled pass above has ~10 us of idle
+        # before every launch)
+        fl = q["flops"] / q["launches"]
+        out["roofline"]["frac_steady"] = round(fl / (steady * 1e-6) / 1e12 / PEAK_TFLOPS, 4)
+        out["roofline"]["steady_launch_us"] = steady
+        out["roofline"]["steady_source"] = ("profiles/ffn_step_timeline_config2.md (rocprofv3 "
+                                            "kernel trace of the event-free pass)")
     for w in (w1, w3, w2):
         w.close()
     # the MFMA rate this board sustains on random fp16 operands under its
