@@ -279,6 +279,9 @@ int lora_xa_fast_slices(int M, int n_cols, int K);
 // The same kernel as a plain split-K bf16 GEMM y = x . W^T of a dense W
 // [N][K] (identity groups, coefficient 1): its slice count.
 int dense_xa_slices(int M, int N, int K);
+// Bytes of f32 partials launch_lora_xa_fast needs for kslices > 1 (whole
+// 256 x 128 tiles per slice, in the kernel's accumulator order); 0 otherwise.
+size_t lora_xa_part_bytes(int M, int n_cols, int kslices);
 hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s);
 hipError_t launch_bf16_to_f16(const uint16_t* x, long long ldx, uint16_t* y,

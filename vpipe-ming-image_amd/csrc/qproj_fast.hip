@@ -971,6 +971,27 @@ __global__ __launch_bounds__(512, 1) void lora_xa_fast_kernel(const LoraXaArgs a
   if (NT - t == 2) body(st1, st2);
 
   if (!live) return;
+  if (kslices > 1) {
+    // The partials in the accumulators' own order: slice ks, tile (row tile,
+    // column block), MFMA wave, fragment f = 8i + 4j + q, lane -- each store
+    // instruction writes 64 lanes x 16 B contiguous (the row-major layout
+    // scattered every instruction over 32 rows). lora_xa_reduce_kernel reads
+    // the same order.
+    const int tiles_c = (a.n_cols + 127) / 128;
+    const long long tile = (long long)(m0 / 256) * tiles_c + c0 / 128;
+    const long long ntiles = (long long)((a.M + 255) / 256) * tiles_c;
+    float4* pw = reinterpret_cast<float4*>(part) + (((ks * ntiles + tile) * 4 + rw) * 32) * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          pw[(8 * i + 4 * j + q) * 64] =
+              make_float4(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                          acc[i][j][4 * q + 3]);
+    return;
+  }
   // D[c][m]: lane owns row m, four consecutive ranks per register quad.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -981,66 +1002,55 @@ __global__ __launch_bounds__(512, 1) void lora_xa_fast_kernel(const LoraXaArgs a
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int c = c0 + 64 * wc + 32 * j + 8 * q + 4 * fk;
-        if (kslices == 1) {
-          const float f = a.coef[c >> 3];
-          uint2 v;
-          if (f == 0.0f) {
-            v = make_uint2(0, 0);
-          } else {
-            v.x = pack_bf16x2_rne(f * acc[i][j][4 * q + 0], f * acc[i][j][4 * q + 1]);
-            v.y = pack_bf16x2_rne(f * acc[i][j][4 * q + 2], f * acc[i][j][4 * q + 3]);
-          }
-          *reinterpret_cast<uint2*>(a.t + (long long)m * a.ldt + c) = v;
+        const float f = a.coef[c >> 3];
+        uint2 v;
+        if (f == 0.0f) {
+          v = make_uint2(0, 0);
         } else {
-          float4 v = make_float4(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1],
-                                 acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-          *reinterpret_cast<float4*>(
-              part + ((long long)ks * a.M + m) * a.n_cols + c) = v;
+          v.x = pack_bf16x2_rne(f * acc[i][j][4 * q + 0], f * acc[i][j][4 * q + 1]);
+          v.y = pack_bf16x2_rne(f * acc[i][j][4 * q + 2], f * acc[i][j][4 * q + 3]);
         }
+        *reinterpret_cast<uint2*>(a.t + (long long)m * a.ldt + c) = v;
       }
     }
   }
 }
 
-// T[m][c] = bf16(coef * sum_s P[s][m][c]), slices summed in order 0..S-1.
-// One thread per 8 columns (one coefficient group): two 16-B loads per
-// slice, one 16-B store when T's rows are 16-B aligned; 32-bit indices (the
-// host keeps M * n_cols / 8 below 2^31).
+// T[m][c] = bf16(coef * sum_s P[s][m][c]), slices summed in order 0..S-1,
+// over the partials in the order lora_xa_fast_kernel writes them: one thread
+// per float4 of a slice (one lane's 4 consecutive ranks of one row), reading
+// the slices' float4s at the same position (every load coalesced) and
+// storing 4 bf16 of T. Positions of row tiles past M or column blocks past
+// n_cols are skipped. 32-bit indices (the host keeps a slice's float4 count
+// below 2^31).
 __global__ void lora_xa_reduce_kernel(const float* part, int kslices, int M,
                                       int n_cols, const LoraXaArgs a) {
-  const unsigned c8n = (unsigned)n_cols >> 3;
-  const unsigned total = (unsigned)M * c8n;
-  const size_t plane = (size_t)M * (size_t)n_cols;
-  const bool st16 = (reinterpret_cast<uintptr_t>(a.t) & 15) == 0 && (a.ldt & 7) == 0;
+  const unsigned tiles_c = ((unsigned)n_cols + 127) / 128;
+  const unsigned ntiles = (((unsigned)M + 255) / 256) * tiles_c;
+  const unsigned total = ntiles * 8192u;             // float4s per slice
+  const float4* p4 = reinterpret_cast<const float4*>(part);
   for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += gridDim.x * blockDim.x) {
-    const unsigned m = i / c8n;
-    const unsigned c = (i - m * c8n) * 8;
-    const float* p = part + (size_t)m * n_cols + c;
-    float4 s0 = *reinterpret_cast<const float4*>(p);
-    float4 s1 = *reinterpret_cast<const float4*>(p + 4);
+    // i = ((tile * 4 + wave) * 32 + f) * 64 + lane, f = 8 fi + 4 fj + fq
+    const unsigned lane = i & 63, f = (i >> 6) & 31, wave = (i >> 11) & 3, tile = i >> 13;
+    const unsigned fr = lane & 31, fk = lane >> 5;
+    const unsigned fi = f >> 3, fj = (f >> 2) & 1, fq = f & 3;
+    const unsigned tm = tile / tiles_c, tc = tile - tm * tiles_c;
+    const unsigned m = 256 * tm + 128 * (wave & 1) + 32 * fi + fr;
+    const unsigned c = 128 * tc + 64 * (wave >> 1) + 32 * fj + 8 * fq + 4 * fk;
+    if (m >= (unsigned)M || c >= (unsigned)n_cols) continue;
+    float4 s = p4[i];
     for (int k = 1; k < kslices; ++k) {
-      p += plane;
-      const float4 v0 = *reinterpret_cast<const float4*>(p);
-      const float4 v1 = *reinterpret_cast<const float4*>(p + 4);
-      s0.x += v0.x; s0.y += v0.y; s0.z += v0.z; s0.w += v0.w;
-      s1.x += v1.x; s1.y += v1.y; s1.z += v1.z; s1.w += v1.w;
+      const float4 v = p4[(size_t)k * total + i];
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
-    const float f = a.coef[c >> 3];
-    uint4 o = make_uint4(0, 0, 0, 0);
-    if (f != 0.0f) {
-      o.x = pack_bf16x2_rne(f * s0.x, f * s0.y);
-      o.y = pack_bf16x2_rne(f * s0.z, f * s0.w);
-      o.z = pack_bf16x2_rne(f * s1.x, f * s1.y);
-      o.w = pack_bf16x2_rne(f * s1.z, f * s1.w);
+    const float co = a.coef[c >> 3];
+    uint2 o = make_uint2(0, 0);
+    if (co != 0.0f) {
+      o.x = pack_bf16x2_rne(co * s.x, co * s.y);
+      o.y = pack_bf16x2_rne(co * s.z, co * s.w);
     }
-    uint16_t* const tp = a.t + (size_t)m * a.ldt + c;
-    if (st16) {
-      *reinterpret_cast<uint4*>(tp) = o;
-    } else {
-      reinterpret_cast<uint2*>(tp)[0] = make_uint2(o.x, o.y);
-      reinterpret_cast<uint2*>(tp)[1] = make_uint2(o.z, o.w);
-    }
+    *reinterpret_cast<uint2*>(a.t + (size_t)m * a.ldt + c) = o;
   }
 }
 
@@ -1253,11 +1263,17 @@ int dense_xa_slices(int M, int N, int K) {
   return ks < 1 ? 1 : ks;
 }
 
+size_t lora_xa_part_bytes(int M, int n_cols, int kslices) {
+  if (kslices <= 1) return 0;
+  return (size_t)kslices * (size_t)((M + 255) / 256) * (size_t)((n_cols + 127) / 128) *
+         (256 * 128 * 4);
+}
+
 hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
                                hipStream_t s) {
   if (a.M <= 0 || a.n_cols <= 0) return hipSuccess;
-  // the reduce's 32-bit indexing: one thread per 8 columns
-  const long long work = (long long)a.M * (a.n_cols / 8);
+  // the reduce's 32-bit indexing: one thread per float4 of a slice
+  const long long work = (long long)((a.M + 255) / 256) * ((a.n_cols + 127) / 128) * 8192;
   if (kslices > 1 && (a.n_cols % 8 != 0 || work >= (1ll << 31))) return hipErrorInvalidValue;
   const unsigned nblk = (unsigned)(((a.M + 255) / 256) * ((a.n_cols + 127) / 128) * kslices);
   hipLaunchKernelGGL(lora_xa_fast_kernel, dim3(nblk), dim3(512), 0, s, a, part, kslices);

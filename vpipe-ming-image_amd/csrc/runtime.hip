@@ -1002,7 +1002,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
   const bool xa_fast = t_cols > 0 && c->route != MING_ROUTE_GENERAL && ldx % 8 == 0 &&
                        (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) && xa_fits;
   const int xa_ks = xa_fast ? ming::lora_xa_fast_slices(M, t_cols, K) : 1;
-  size_t part_bytes = xa_ks > 1 ? (size_t)xa_ks * M * t_cols * 4 : 0;
+  size_t part_bytes = ming::lora_xa_part_bytes(M, t_cols, xa_ks);
   // Which projections take the fast route. It addresses each operand as a
   // 64-bit base plus 32-bit byte offsets: x (fp16 copy, row stride K), T and
   // every B stack must fit.
@@ -1048,8 +1048,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
         (uint64_t)q->N * (uint64_t)K * 2 <= (1ull << 32);
     if (dense_sk) {
       dense_ks[i] = ming::dense_xa_slices(M, q->N, K);
-      if (dense_ks[i] > 1)
-        part_bytes = std::max(part_bytes, (size_t)dense_ks[i] * M * q->N * 4);
+      part_bytes = std::max(part_bytes, ming::lora_xa_part_bytes(M, q->N, dense_ks[i]));
     }
     if (o.gate && !fast[i]) up_bytes = std::max(up_bytes, (size_t)M * q->N * 2);
   }
