@@ -62,8 +62,25 @@ __device__ __forceinline__ void attn_sync() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-__device__ __forceinline__ float xor32(float v) {
-  return __shfl_xor(v, 32, 64);
+// A value and its twin in the other lane half (lane ^ 32) combined by gfx950's
+// v_permlane32_swap: after the swap the two results hold, in every lane, the
+// lane-half-0 and lane-half-1 values of the pair, so their sum or max is the
+// pair's in either order (no LDS round trip, as a bpermute takes).
+__device__ __forceinline__ void halves(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum32(float v) {
+  float a, b;
+  halves(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float max32(float v) {
+  float a, b;
+  halves(v, a, b);
+  return fmaxf(a, b);
 }
 
 __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
@@ -116,7 +133,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) t2[s] = t4[s] + t4[s ^ 2];
     const float t1 = t2[0] + t2[1];
-    const float inv = head_rms_inv(t1 + xor32(t1), a.eps);
+    const float inv = head_rms_inv(sum32(t1), a.eps);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       qf[s].x = norm_rope_pair(qf[s].x, qwv[s].x, inv, qcs[s].x, qsn[s].x);
@@ -240,7 +257,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[t][r]);
-    mloc = fmaxf(mloc, xor32(mloc)) * sl2;            // sl2 > 0: max commutes
+    mloc = max32(mloc) * sl2;                         // sl2 > 0: max commutes
     if (__any(mloc > mref + kLazy)) {
       const float mnew = fmaxf(mref, mloc);
       const float alpha = __builtin_amdgcn_exp2f(mref - mnew);
@@ -310,7 +327,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const AttnArgs a) {
   }
   attn_sync();                                     // no DMA outlives the block
 
-  const float ltot = lrun + xor32(lrun);
+  const float ltot = sum32(lrun);
   const float inv = 1.0f / ltot;
   const int q = q0 + 32 * wave + fr;
   if (q < R) {
