@@ -1017,40 +1017,54 @@ __global__ __launch_bounds__(512, 1) void lora_xa_fast_kernel(const LoraXaArgs a
 }
 
 // T[m][c] = bf16(coef * sum_s P[s][m][c]), slices summed in order 0..S-1,
-// over the partials in the order lora_xa_fast_kernel writes them: one thread
-// per float4 of a slice (one lane's 4 consecutive ranks of one row), reading
-// the slices' float4s at the same position (every load coalesced) and
-// storing 4 bf16 of T. Positions of row tiles past M or column blocks past
-// n_cols are skipped. 32-bit indices (the host keeps a slice's float4 count
-// below 2^31).
+// over the partials in the order lora_xa_fast_kernel writes them. One thread
+// per row and 8 consecutive ranks: the float4s of accumulator lanes fr and
+// fr + 32 (ranks 8q + 0..3 and 8q + 4..7 of one row), read from every slice
+// at the same positions (32 threads cover each 1-KB run, every load
+// coalesced), one 16-byte store of T. Positions of row tiles past M or
+// column blocks past n_cols are skipped. 32-bit indices (the host keeps a
+// slice's float4 count below 2^31).
 __global__ void lora_xa_reduce_kernel(const float* part, int kslices, int M,
                                       int n_cols, const LoraXaArgs a) {
   const unsigned tiles_c = ((unsigned)n_cols + 127) / 128;
   const unsigned ntiles = (((unsigned)M + 255) / 256) * tiles_c;
   const unsigned total = ntiles * 8192u;             // float4s per slice
+  const bool st16 = (reinterpret_cast<uintptr_t>(a.t) & 15) == 0 && (a.ldt & 7) == 0;
   const float4* p4 = reinterpret_cast<const float4*>(part);
-  for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += gridDim.x * blockDim.x) {
-    // i = ((tile * 4 + wave) * 32 + f) * 64 + lane, f = 8 fi + 4 fj + fq
-    const unsigned lane = i & 63, f = (i >> 6) & 31, wave = (i >> 11) & 3, tile = i >> 13;
-    const unsigned fr = lane & 31, fk = lane >> 5;
+  for (unsigned t = blockIdx.x * blockDim.x + threadIdx.x; t < total / 2;
+       t += gridDim.x * blockDim.x) {
+    // the float4 of accumulator lane fr: ((tile * 4 + wave) * 32 + f) * 64 + fr,
+    // f = 8 fi + 4 fj + fq; lane fr + 32 is 32 float4s on
+    const unsigned fr = t & 31, g = t >> 5;
+    const unsigned i = g * 64 + fr;
+    const unsigned f = g & 31, wave = (g >> 5) & 3, tile = g >> 7;
     const unsigned fi = f >> 3, fj = (f >> 2) & 1, fq = f & 3;
     const unsigned tm = tile / tiles_c, tc = tile - tm * tiles_c;
     const unsigned m = 256 * tm + 128 * (wave & 1) + 32 * fi + fr;
-    const unsigned c = 128 * tc + 64 * (wave >> 1) + 32 * fj + 8 * fq + 4 * fk;
+    const unsigned c = 128 * tc + 64 * (wave >> 1) + 32 * fj + 8 * fq;
     if (m >= (unsigned)M || c >= (unsigned)n_cols) continue;
-    float4 s = p4[i];
+    float4 s0 = p4[i], s1 = p4[i + 32];
     for (int k = 1; k < kslices; ++k) {
-      const float4 v = p4[(size_t)k * total + i];
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+      const float4 v0 = p4[(size_t)k * total + i];
+      const float4 v1 = p4[(size_t)k * total + i + 32];
+      s0.x += v0.x; s0.y += v0.y; s0.z += v0.z; s0.w += v0.w;
+      s1.x += v1.x; s1.y += v1.y; s1.z += v1.z; s1.w += v1.w;
     }
     const float co = a.coef[c >> 3];
-    uint2 o = make_uint2(0, 0);
+    uint4 o = make_uint4(0, 0, 0, 0);
     if (co != 0.0f) {
-      o.x = pack_bf16x2_rne(co * s.x, co * s.y);
-      o.y = pack_bf16x2_rne(co * s.z, co * s.w);
+      o.x = pack_bf16x2_rne(co * s0.x, co * s0.y);
+      o.y = pack_bf16x2_rne(co * s0.z, co * s0.w);
+      o.z = pack_bf16x2_rne(co * s1.x, co * s1.y);
+      o.w = pack_bf16x2_rne(co * s1.z, co * s1.w);
     }
-    *reinterpret_cast<uint2*>(a.t + (size_t)m * a.ldt + c) = o;
+    uint16_t* const tp = a.t + (size_t)m * a.ldt + c;
+    if (st16) {
+      *reinterpret_cast<uint4*>(tp) = o;
+    } else {
+      reinterpret_cast<uint2*>(tp)[0] = make_uint2(o.x, o.y);
+      reinterpret_cast<uint2*>(tp)[1] = make_uint2(o.z, o.w);
+    }
   }
 }
 
@@ -1279,7 +1293,7 @@ hipError_t launch_lora_xa_fast(const LoraXaArgs& a, float* part, int kslices,
   hipLaunchKernelGGL(lora_xa_fast_kernel, dim3(nblk), dim3(512), 0, s, a, part, kslices);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || kslices == 1) return e;
-  long long blocks = (work + 255) / 256;
+  long long blocks = (work / 2 + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(lora_xa_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
                      part, kslices, a.M, a.n_cols, a);
