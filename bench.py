@@ -712,6 +712,9 @@ def main():
                      "achieved": round(achieved, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
                      "traffic": measured_traffic(),
+                     "traffic_source": ("profiles/qproj_w4_ffn_config2_traffic.md (rocprofv3 "
+                                        "FETCH_SIZE + WRITE_SIZE passes of this command, scaled "
+                                        "by a 256 MiB copy)"),
                      "avg_launch_us": round(1e3 * q["ms"] / q["launches"], 2),
                      "flop_per_launch": round(q["flops"] / q["launches"])},
         "kernels": kernels,
