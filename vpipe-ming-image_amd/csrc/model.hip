@@ -572,11 +572,12 @@ int ming_model_forward(ming_model* m, const uint16_t* latents, const uint16_t* c
   const int H = d.hidden, JT = IMG + CAP;
   // the layout is checked, not trusted (ming-dit.cc:1507-1523)
   if (IMG <= 0 || CAP <= 0 || Q < 0 || Q > CAP)
-    return rt_fail(MING_ERR_SHAPE, "ming_model_forward: the layout does not add up");
+    return rt_fail(MING_ERR_SHAPE, "ming_model_forward: image and caption row counts must be "
+                                   "positive, with 0 <= query rows <= caption rows");
   if ((Q > 0 && cap_stride < d.cap_dim) || (CAP > Q && cap_stride < H) || cap_stride % 8)
     return rt_fail(MING_ERR_SHAPE,
-                   "ming_model_forward: the caption's row stride is narrower than a row "
-                   "it carries (or not a multiple of 8)");
+                   "ming_model_forward: cap_stride must be a multiple of 8 and at least "
+                   "cap_dim (query rows) and the hidden width (pass-through rows)");
   for (int t = 0; t < JT; ++t)
     if (pos_t[t] < 0 || pos_h[t] < 0 || pos_w[t] < 0 || pos_t[t] >= d.axes_lens[0] ||
         pos_h[t] >= d.axes_lens[1] || pos_w[t] >= d.axes_lens[2])

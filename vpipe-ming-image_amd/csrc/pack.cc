@@ -215,8 +215,8 @@ int check_dense_shapes(const ming_pack* p) {
     const ming::st::Tensor* t = p->tensors.find(x.name);
     if (!t || t->shape.size() != 2 || t->shape[0] != x.rows || t->shape[1] != x.cols)
       return rt_fail(MING_ERR_SHAPE,
-                     x.name + (t ? " does not have the shape [" + std::to_string(x.rows) + ", " +
-                                       std::to_string(x.cols) + "] the config implies"
+                     x.name + (t ? ": expected " + std::to_string(x.rows) + " x " +
+                                       std::to_string(x.cols) + " from config.json"
                                  : " is missing"));
   }
   return MING_OK;
