@@ -341,7 +341,7 @@ def test_load_refuses_what_it_does_not_run(ctx, tmp_path):
         m.Model.load(ctx, d)
     d = str(tmp_path / "short")
     make_checkpoint(d, seed=12, cfg=CFG, shards=1, drop=("layers.1.ffn_norm2.weight",))
-    with pytest.raises(m.MingError, match="layers.1.ffn_norm2.weight' is not in the checkpoint"):
+    with pytest.raises(m.MingError, match="layers.1.ffn_norm2.weight' is absent from the checkpoint"):
         m.Model.load(ctx, d)
 
 

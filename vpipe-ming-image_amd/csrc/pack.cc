@@ -327,7 +327,7 @@ struct Loader {
 
   const ming::st::Tensor* need(const std::string& n, int* rc) {
     const ming::st::Tensor* t = p->tensors.find(n);
-    if (!t) *rc = rt_fail(MING_ERR_SHAPE, "ming_model_load: '" + n + "' is not in the checkpoint");
+    if (!t) *rc = rt_fail(MING_ERR_SHAPE, "ming_model_load: '" + n + "' is absent from the checkpoint");
     return t;
   }
 
