@@ -1,9 +1,9 @@
 """A projection whose input is larger than 4 GiB: 600,000 rows x 3840 bf16
 (4.6 GB). The fast route addresses x's fp16 copy with 32-bit byte offsets
-from a 64-bit base, so the host must refuse it there and run the general
-kernels, which index in 64 bits; the x.A takes its general kernel the same
-way. Held to the oracle on rows spread over the whole input, the last rows
-past the 4 GiB mark among them."""
+from a 64-bit base and takes operands within 2 GiB only, so the host must
+refuse it there and run the general kernels, which index in 64 bits; the x.A
+takes its general kernel the same way. Held to the oracle on rows spread
+over the whole input, rows past the 2 GiB and 4 GiB marks among them."""
 import numpy as np
 import pytest
 
@@ -34,7 +34,7 @@ def test_input_beyond_4_gib_runs_the_general_kernels(ctx, orc):
     torch.cuda.synchronize()
     eng = ctx.engagement()
     assert eng["gemm_q4"] == 1 and eng["lora_proj"] == 1
-    assert eng["gemm_fast"] == 0                    # past the fast route's 32-bit offsets
+    assert eng["gemm_fast"] == 0                    # past the fast route's offset range
     rows = np.array([0, 1, 12_345, 280_000, 559_239, 559_240, 599_000, M - 2, M - 1])
     ri = torch.from_numpy(rows).cuda()
     xs = from_dev(x.index_select(0, ri))

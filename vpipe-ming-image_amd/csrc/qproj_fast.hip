@@ -215,8 +215,9 @@ __device__ __forceinline__ void qproj_fast_body(const QprojArgs& a) {
 
   // DMA sources for this lane, per stage (advance by k).
   // x tile: wave issues chunks q = 8*wave + i; lane p = 64q + lane.
-  // Byte offsets from the stage's base (the host keeps every tile inside
-  // 4 GiB of its base, so they fit 32 bits).
+  // Byte offsets from the stage's base (the host keeps every operand
+  // within 2 GiB of its base, so they fit 31 bits whether the hardware reads
+  // the offset as signed or unsigned).
   uint32_t xoff[XD];
 #pragma unroll
   for (int i = 0; i < XD; ++i) {

@@ -938,7 +938,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       int rc = build_stacks(q);
       if (rc != MING_OK) return rc;
       xa.A[i] = q->A_all;
-      if ((uint64_t)q->a_rows * (uint64_t)q->K * 2 > (1ull << 32)) xa_fits = false;
+      if ((uint64_t)q->a_rows * (uint64_t)q->K * 2 > (1ull << 31)) xa_fits = false;
     }
     int qp_groups = 0;
     for (int si = 0; si < nseg; ++si) {
@@ -1000,7 +1000,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
   // the fast x.A addresses x and each A stack as 64-bit bases plus 32-bit
   // byte offsets; its K split (slices summed in f32 by a second launch)
   const bool xa_fast = t_cols > 0 && c->route != MING_ROUTE_GENERAL && ldx % 8 == 0 &&
-                       (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) && xa_fits;
+                       (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 31) && xa_fits;
   const int xa_ks = xa_fast ? ming::lora_xa_fast_slices(M, t_cols, K) : 1;
   size_t part_bytes = ming::lora_xa_part_bytes(M, t_cols, xa_ks);
   // Which projections take the fast route. It addresses each operand as a
@@ -1010,11 +1010,11 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
   bool any_fast = false;
   for (int i = 0; i < n; ++i) {
     const ming_qweight* q = qs[i];
-    bool fits32 = (uint64_t)M * (uint64_t)K * 2 <= (1ull << 32) &&
-                  (uint64_t)M * (uint64_t)t_cols * 2 <= (1ull << 32);
+    bool fits32 = (uint64_t)M * (uint64_t)K * 2 <= (1ull << 31) &&
+                  (uint64_t)M * (uint64_t)t_cols * 2 <= (1ull << 31);
     for (int si = 0; si < (int)q->segs.size() && t_cols > 0; ++si)
       if (qa[i].seg[si].chunks > 0 &&
-          (uint64_t)q->segs[si].N * (uint64_t)q->b_ld[si] * 2 > (1ull << 32))
+          (uint64_t)q->segs[si].N * (uint64_t)q->b_ld[si] * 2 > (1ull << 31))
         fits32 = false;
     fast[i] = q->bits != 16 && q->fast && c->route == MING_ROUTE_AUTO && fits32;
     any_fast = any_fast || fast[i];
@@ -1044,8 +1044,8 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     const bool dense_sk =
         q->bits == 16 && c->route != MING_ROUTE_GENERAL && live_segs[i] == 0 && !o.gate &&
         !o.yh && tiles < 64 && q->N % 64 == 0 && q->N <= 8 * ming::kMaxGroups &&
-        K % 64 == 0 && o.ldy <= (1 << 30) && (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 32) &&
-        (uint64_t)q->N * (uint64_t)K * 2 <= (1ull << 32);
+        K % 64 == 0 && o.ldy <= (1 << 30) && (uint64_t)M * (uint64_t)ldx * 2 <= (1ull << 31) &&
+        (uint64_t)q->N * (uint64_t)K * 2 <= (1ull << 31);
     if (dense_sk) {
       dense_ks[i] = ming::dense_xa_slices(M, q->N, K);
       part_bytes = std::max(part_bytes, ming::lora_xa_part_bytes(M, q->N, dense_ks[i]));
