@@ -46,11 +46,13 @@ def test_residuals(ctx, orc, gated):
         term = f32(sub).astype(np.float64)
     sync()
     got = from_dev(hd)
-    # tanhf may differ by an f32 ulp between the GPU and glibc; near
-    # cancellation that is many ulps of the sum, so bound by the operands
+    # The kernel rounds the product, then the sum, as the oracle does; tanhf
+    # may still differ by an f32 ulp between the GPU and glibc, which near
+    # cancellation is many ulps of the sum, so bound by the operands. Such
+    # elements are rare (measured: 2e-5 of them).
     mag = np.abs(f32(h)) + np.abs(term)
     assert np.all(np.abs(f32(got) - f32(want)) <= 2.0 ** -8 * mag + 1e-30)
-    assert (got != want).mean() < 1e-2
+    assert (got != want).mean() < 1e-3
 
 
 def test_modulate_is_fold_gain(ctx, orc):

@@ -91,15 +91,18 @@ def test_qk_norm_rope_parity(ctx, orc, rows, n_heads, ld_extra):
     assert ctx.engagement()["qk_norm_rope"] == 1
     got = from_dev(xd)
     want = orc.qk_norm_rope(x, 0, n_heads * Hd, n_heads, Hd, wq, wk, c, s)
-    # A one-ulp difference in a normalized input (f32 sum order) moves a
-    # rotated output by up to an ulp of the PAIR's magnitude, which near
-    # cancellation (a*c ~ b*s) is many ulps of the output itself. So the
-    # element bound is 2 bf16 ulps of the pair norm the rotation preserves.
+    # The kernel rounds where the oracle does (each product of the rotation,
+    # then the sum); only the head's sum of squares runs in another order.
+    # A one-ulp difference in a normalized input moves a rotated output by
+    # up to an ulp of the PAIR's magnitude, which near cancellation
+    # (a*c ~ b*s) is many ulps of the output itself. So the element bound is
+    # 2 bf16 ulps of the pair norm the rotation preserves, and such elements
+    # are rare (measured: 3e-6 of them at 4352 rows).
     g2 = f32(got)[:, :2 * n_heads * Hd].reshape(rows, -1, 2)
     w2 = f32(want)[:, :2 * n_heads * Hd].reshape(rows, -1, 2)
     pn = np.sqrt((w2.astype(np.float64) ** 2).sum(-1, keepdims=True))
     assert np.all(np.abs(g2 - w2) <= 2.0 ** -6 * pn + 1e-30)
-    assert (_ulps(got, want) > 0).mean() < 0.02
+    assert (_ulps(got, want) > 0).mean() < 1e-3
     assert orc.rel_l2(f32(got), f32(want)) <= TOL
     # untouched columns past q and k
     assert np.array_equal(got[:, 2 * n_heads * Hd:], x[:, 2 * n_heads * Hd:])
@@ -151,8 +154,12 @@ def test_llm_qk_norm_rope_parity(ctx, orc, rows, n_q, n_k, n_v, rot_half, norm):
     nh = (n_q + n_k) * 128
     assert np.array_equal(got[:, nh:], x[:, nh:])           # the values and the tail
     u = _ulps(got[:, :nh], want[:, :nh])
+    if not norm:
+        # the rotation alone: each product rounded, then the sum, as the
+        # oracle rounds -- the same bits
+        assert np.array_equal(got, want)
     if rot_half == 0:
-        assert u.max() <= 1 and (u > 0).mean() < 0.01
+        assert u.max() <= 1 and (u > 0).mean() < 1e-3
     else:
         # a one-ulp difference in a normalized input moves a rotated output by
         # up to an ulp of its pair's magnitude: bound each element by 2 bf16
@@ -163,7 +170,7 @@ def test_llm_qk_norm_rope_parity(ctx, orc, rows, n_q, n_k, n_v, rot_half, norm):
         pn = np.sqrt(w[..., :R] ** 2 + w[..., R:2 * R] ** 2)
         pn = np.concatenate([pn, pn], axis=-1)
         assert np.all(np.abs(g[..., :2 * R] - w[..., :2 * R]) <= 2.0 ** -6 * pn + 1e-30)
-        assert (u > 0).mean() < 0.02
+        assert (u > 0).mean() < 1e-3
         if R == 32:
             assert _ulps(got[:, :nh].reshape(rows, -1, 128)[..., 64:],
                          want[:, :nh].reshape(rows, -1, 128)[..., 64:]).max() <= 1

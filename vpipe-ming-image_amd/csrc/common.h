@@ -120,14 +120,16 @@ __device__ __forceinline__ float head_rms_inv(float ss, float eps) {
 }
 // One interleaved pair (x0, x1): normalized with weight pair w, rounded to
 // bf16 (the reference stores the norm), rotated by (c, s) as
-// (x0 + i x1)(c + i s), packed to bf16.
+// (x0 + i x1)(c + i s), packed to bf16. Every product is rounded before its
+// sum (no contraction into an FMA), as the formula is written: the bits then
+// follow the source, not the compiler's choice per call site.
 __device__ __forceinline__ uint32_t norm_rope_pair(uint32_t u, uint32_t w, float inv, float c,
                                                    float s) {
-  const uint32_t nb = pack_bf16x2_rne(__fmul_rn(__fmul_rn(bf16_lo(u), inv), bf16_lo(w)),
-                                      __fmul_rn(__fmul_rn(bf16_hi(u), inv), bf16_hi(w)));
+#pragma clang fp contract(off)
+  const uint32_t nb = pack_bf16x2_rne(bf16_lo(u) * inv * bf16_lo(w), bf16_hi(u) * inv * bf16_hi(w));
   const float a = bf16_lo(nb), b = bf16_hi(nb);
-  const float re = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-  const float im = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+  const float re = a * c - b * s;
+  const float im = a * s + b * c;
   return pack_bf16x2_rne(re, im);
 }
 

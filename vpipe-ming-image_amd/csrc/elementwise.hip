@@ -112,13 +112,13 @@ __global__ void residual_kernel(uint16_t* h, long long ldh, const uint16_t* gate
     uint32_t* op = &o.x;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
       float s0 = bf16_lo(sp[e]), s1 = bf16_hi(sp[e]);
       if (mode == 0) {
-        s0 = __fmul_rn(tanhf(bf16_lo(gp[e])), s0);
-        s1 = __fmul_rn(tanhf(bf16_hi(gp[e])), s1);
+        s0 = tanhf(bf16_lo(gp[e])) * s0;
+        s1 = tanhf(bf16_hi(gp[e])) * s1;
       }
-      op[e] = pack_bf16x2(__fadd_rn(bf16_lo(hp[e]), s0),
-                          __fadd_rn(bf16_hi(hp[e]), s1));
+      op[e] = pack_bf16x2(bf16_lo(hp[e]) + s0, bf16_hi(hp[e]) + s1);
     }
     *reinterpret_cast<uint4*>(h + r * ldh + c) = o;
   }

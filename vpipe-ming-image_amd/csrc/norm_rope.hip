@@ -124,12 +124,13 @@ __global__ __launch_bounds__(256, 5) void rmsnorm_kernel(
         uint32_t* rp = &r.x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
           float s0 = bf16_lo(ou[e]), s1 = bf16_hi(ou[e]);
           if (MODE == 2) {
-            s0 = __fmul_rn(t[2 * e], s0);
-            s1 = __fmul_rn(t[2 * e + 1], s1);
+            s0 = t[2 * e] * s0;
+            s1 = t[2 * e + 1] * s1;
           }
-          rp[e] = pack_bf16x2_rne(__fadd_rn(bf16_lo(hp[e]), s0), __fadd_rn(bf16_hi(hp[e]), s1));
+          rp[e] = pack_bf16x2_rne(bf16_lo(hp[e]) + s0, bf16_hi(hp[e]) + s1);
         }
         *reinterpret_cast<uint4*>(h + (long long)row * ldh + 8 * c) = r;
       }
@@ -210,12 +211,13 @@ __global__ __launch_bounds__(256, 5) void norm_residual_norm_kernel(
       uint32_t* hp = &hv[i].x;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
         float s0 = bf16_lo(ou[e]), s1 = bf16_hi(ou[e]);
         if constexpr (GATED) {
-          s0 = __fmul_rn(t[2 * e], s0);
-          s1 = __fmul_rn(t[2 * e + 1], s1);
+          s0 = t[2 * e] * s0;
+          s1 = t[2 * e + 1] * s1;
         }
-        hp[e] = pack_bf16x2_rne(__fadd_rn(bf16_lo(hp[e]), s0), __fadd_rn(bf16_hi(hp[e]), s1));
+        hp[e] = pack_bf16x2_rne(bf16_lo(hp[e]) + s0, bf16_hi(hp[e]) + s1);
       }
       *reinterpret_cast<uint4*>(h + rr * ldh + 8 * c) = hv[i];
       // the next norm's sum of squares, in rmsnorm_kernel's order
@@ -426,8 +428,8 @@ __global__ __launch_bounds__(256) void llm_qk_norm_rope_kernel(
         const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          a[e] = low ? __fsub_rn(__fmul_rn(a[e], c[e]), __fmul_rn(b[e], s[e]))
-                     : __fadd_rn(__fmul_rn(a[e], c[e]), __fmul_rn(b[e], s[e]));
+#pragma clang fp contract(off)
+          a[e] = low ? a[e] * c[e] - b[e] * s[e] : a[e] * c[e] + b[e] * s[e];
         }
       }
     }
