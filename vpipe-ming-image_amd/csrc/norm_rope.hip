@@ -288,54 +288,66 @@ __global__ void rope_table_kernel(const int32_t* pt, const int32_t* ph,
   sin_t[idx] = (float)sin(ang);
 }
 
-// One 16-lane group per (row, head) of q or k; each lane owns 8 elements
-// (4 interleaved pairs) of the 128-wide head. Block (x, y): heads 16x ..
-// 16x + 15 of the row's 2 * n_heads (q then k) over QK_RPB consecutive rows,
-// row groups strided by the grid's y extent, so no index division. The
-// kernel is near the memory bound with a heavy VALU share, so both bf16
-// roundings of a pair take gfx950's v_cvt_pk_bf16_f32 (round to nearest
-// even: the bits of the bit-twiddled rounding for every non-NaN value), and
-// the loads of all QK_RPB rows are issued before the first reduction: four
-// rows a block read [4352, 2 x 3840] in 26.1 us against 31.0 us at one row
-// a block (5.1 against 4.3 TB/s, measured on the MI355X).
-constexpr int QK_RPB = 4;
+// A 16-lane group owns the same 8 elements (4 interleaved pairs) of QK_HPL
+// heads of a row, so the row's cos / sin load once per QK_HPL heads; block
+// (x, y): heads 16 * QK_HPL * x .. of the row's q then k heads, over QK_RPB
+// consecutive rows, row groups strided by the grid's y extent (no index
+// division). The loads of all QK_RPB rows are issued before the first
+// reduction, and both bf16 roundings of a pair take gfx950's
+// v_cvt_pk_bf16_f32 (round to nearest even: the bits of the bit-twiddled
+// rounding for every non-NaN value). Measured on the MI355X, [4352, 2 x 3840]
+// in place: one head a group over 4 rows 31.2 us, two heads over 2 rows
+// 29.4 us (the same bits).
+constexpr int QK_RPB = 2, QK_HPL = 2;
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     uint16_t* __restrict__ x, long long ld, int q_col, int k_col, int rows,
     int nq, int nk, const uint16_t* __restrict__ wq,
     const uint16_t* __restrict__ wk, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, float eps) {
   const int tid = threadIdx.x, lane = tid & 63;
-  const int hh0 = (int)blockIdx.x * 16 + (tid >> 4);
   const int sub = lane & 15;
-  const bool live = hh0 < nq + nk;
-  const int hh = live ? hh0 : 0;
-  const bool isk = hh >= nq;
-  const int head = isk ? hh - nq : hh;
-  const int col = (isk ? k_col : q_col) + head * 128 + 8 * sub;
-  const uint4 wv = *reinterpret_cast<const uint4*>((isk ? wk : wq) + 8 * sub);
+  const int grp = (int)blockIdx.x * 16 + (tid >> 4);
+  const uint4 wqv = *reinterpret_cast<const uint4*>(wq + 8 * sub);
+  const uint4 wkv = *reinterpret_cast<const uint4*>(wk + 8 * sub);
+  int col[QK_HPL];
+  bool live[QK_HPL], isk[QK_HPL];
+#pragma unroll
+  for (int h = 0; h < QK_HPL; ++h) {
+    const int hh0 = grp * QK_HPL + h;
+    live[h] = hh0 < nq + nk;
+    const int hh = live[h] ? hh0 : 0;   // a dead slot reads head 0 and stores nothing
+    isk[h] = hh >= nq;
+    col[h] = (isk[h] ? k_col + (hh - nq) * 128 : q_col + hh * 128) + 8 * sub;
+  }
   for (int r0 = (int)blockIdx.y * QK_RPB; r0 < rows; r0 += (int)gridDim.y * QK_RPB) {
-    uint4 v[QK_RPB];
+    uint4 v[QK_RPB][QK_HPL];
     float4 cv[QK_RPB], sv[QK_RPB];
 #pragma unroll
     for (int j = 0; j < QK_RPB; ++j) {
       const int row = r0 + j < rows ? r0 + j : rows - 1;   // the tail re-reads a valid row
-      v[j] = *reinterpret_cast<const uint4*>(x + (long long)row * ld + col);
+#pragma unroll
+      for (int h = 0; h < QK_HPL; ++h)
+        v[j][h] = *reinterpret_cast<const uint4*>(x + (long long)row * ld + col[h]);
       cv[j] = *reinterpret_cast<const float4*>(cos_t + (long long)row * 64 + 4 * sub);
       sv[j] = *reinterpret_cast<const float4*>(sin_t + (long long)row * 64 + 4 * sub);
     }
 #pragma unroll
     for (int j = 0; j < QK_RPB; ++j) {
-      float ss = head_ss8(v[j]);
 #pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      const float inv = head_rms_inv(ss, eps);
-      uint4 o;
-      o.x = norm_rope_pair(v[j].x, wv.x, inv, cv[j].x, sv[j].x);
-      o.y = norm_rope_pair(v[j].y, wv.y, inv, cv[j].y, sv[j].y);
-      o.z = norm_rope_pair(v[j].z, wv.z, inv, cv[j].z, sv[j].z);
-      o.w = norm_rope_pair(v[j].w, wv.w, inv, cv[j].w, sv[j].w);
-      if (live && r0 + j < rows)
-        *reinterpret_cast<uint4*>(x + (long long)(r0 + j) * ld + col) = o;
+      for (int h = 0; h < QK_HPL; ++h) {
+        float ss = head_ss8(v[j][h]);
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float inv = head_rms_inv(ss, eps);
+        const uint4 wv = isk[h] ? wkv : wqv;
+        uint4 o;
+        o.x = norm_rope_pair(v[j][h].x, wv.x, inv, cv[j].x, sv[j].x);
+        o.y = norm_rope_pair(v[j][h].y, wv.y, inv, cv[j].y, sv[j].y);
+        o.z = norm_rope_pair(v[j][h].z, wv.z, inv, cv[j].z, sv[j].z);
+        o.w = norm_rope_pair(v[j][h].w, wv.w, inv, cv[j].w, sv[j].w);
+        if (live[h] && r0 + j < rows)
+          *reinterpret_cast<uint4*>(x + (long long)(r0 + j) * ld + col[h]) = o;
+      }
     }
   }
 }
@@ -532,7 +544,8 @@ hipError_t launch_qk_norm_rope(uint16_t* x, long long ld, int q_col,
   if (rows <= 0 || n_heads <= 0) return hipSuccess;
   const int groups = (rows + QK_RPB - 1) / QK_RPB;
   const unsigned gy = (unsigned)(groups < 65535 ? groups : 65535);   // grid y limit; groups stride
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((2 * n_heads + 15) / 16), gy),
+  hipLaunchKernelGGL(qk_norm_rope_kernel,
+                     dim3((unsigned)((2 * n_heads + 16 * QK_HPL - 1) / (16 * QK_HPL)), gy),
                      dim3(256), 0, s, x, ld, q_col, k_col, rows, n_heads, n_heads, wq,
                      wk, cos_t, sin_t, eps);
   return hipGetLastError();
@@ -544,7 +557,8 @@ hipError_t launch_k_norm_rope(uint16_t* x, long long ld, int k_col, int rows, in
   if (rows <= 0 || n_heads <= 0) return hipSuccess;
   const int groups = (rows + QK_RPB - 1) / QK_RPB;
   const unsigned gy = (unsigned)(groups < 65535 ? groups : 65535);
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((n_heads + 15) / 16), gy),
+  hipLaunchKernelGGL(qk_norm_rope_kernel,
+                     dim3((unsigned)((n_heads + 16 * QK_HPL - 1) / (16 * QK_HPL)), gy),
                      dim3(256), 0, s, x, ld, k_col, k_col, rows, 0, n_heads, wk, wk,
                      cos_t, sin_t, eps);
   return hipGetLastError();
