@@ -410,7 +410,9 @@ def time_forward_2048(model, torch, gen, steps):
 def time_norms(ctx, torch, gen, rounds=4):
     """The HBM-bound feeds at configs[2]'s shape (4352 rows, H 3840, 30 heads):
     RMSNorm [4352, 3840] out of place, and qk-norm + RoPE in place on the
-    token-major [4352, 3*3840] qkv plane. Each kernel walks a ring of
+    token-major [4352, 3*3840] qkv plane -- the DiT's interleaved-pair form,
+    and the encoder's LlmOps form on the same plane (30 query then 30 key
+    heads from column 0, both weights, rotate-half width 64). Each kernel walks a ring of
     buffers totalling more than the 256 MB Infinity Cache (MALL), so every
     launch reads its input from HBM, not from a cache the previous launch
     filled; the launches of a round are bracketed by two events on the
@@ -444,11 +446,17 @@ def time_norms(ctx, torch, gen, rounds=4):
     def run_qk(i):
         ctx.qk_norm_rope(qkvs[i % n_qk], 3 * H, 0, H, rows, NH, nq, nk, cos_t, sin_t)
 
+    def run_llm_qk(i):
+        ctx.llm_qk_norm_rope(qkvs[i % n_qk], nq, nk, cos_t, sin_t, rows, 3 * H, NH, NH, 64,
+                             1e-6)
+
     out = {}
     for name, fn, nbuf, shape, nbytes, ring in (
             ("rmsnorm", run_rms, n_rms, [rows, H], 4.0 * rows * H + 2.0 * H,
              n_rms * 4 * rows * H),
             ("qk_norm_rope", run_qk, n_qk, [rows, 2 * H], 8.0 * rows * H + 512.0,
+             n_qk * 6 * rows * H),
+            ("llm_qk_norm_rope", run_llm_qk, n_qk, [rows, 2 * H], 8.0 * rows * H + 512.0,
              n_qk * 6 * rows * H)):
         for i in range(2 * nbuf):                 # warm: every buffer touched
             fn(i)
