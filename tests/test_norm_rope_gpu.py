@@ -69,7 +69,10 @@ def test_rope_table_parity(ctx, orc):
 
 
 @pytest.mark.parametrize("rows,n_heads,ld_extra", [(300, 30, 0), (4352, 30, 3840),
-                                                   (33, 2, 0)])
+                                                   (33, 2, 0),
+                                                   # more row pairs than the grid's y
+                                                   # extent (65535): the grid-stride loop
+                                                   (140000, 1, 0)])
 def test_qk_norm_rope_parity(ctx, orc, rows, n_heads, ld_extra):
     print(f"case qk_norm_rope rows={rows} heads={n_heads}", flush=True)
     import torch
@@ -122,7 +125,7 @@ def _llm_tables(rows, R, theta=10000.0):
     (257, 14, 2, 2, 32, True),        # partial rotary: dims 64..127 pass through
     (100, 8, 8, 0, 0, True),          # norm only
     (100, 8, 2, 2, 64, False),        # rotation only
-    (70000, 1, 1, 1, 32, True),       # more rows than the grid's y extent
+    (140000, 1, 1, 1, 32, True),      # more row pairs than the grid's y extent (65535)
 ])
 def test_llm_qk_norm_rope_parity(ctx, orc, rows, n_q, n_k, n_v, rot_half, norm):
     """LlmOps::qk_norm_rope (ming-ops.h:118-122; ming_llm.metal:100-178)
