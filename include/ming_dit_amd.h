@@ -200,6 +200,17 @@ int ming_lin(ming_ctx* ctx, const ming_qweight* qw, const uint16_t* x,
              int64_t ldx, uint16_t* y, int64_t ldy, int M,
              const float* scales);
 
+/* ming_lin with a bias: y = bf16(x . W^T + (live LoRA) + bias), the bias
+ * added to the f32 result before the output's one rounding, as the LLM
+ * encoder's LlmOps::linear(enc, x, xe, w, bias, y, ye, M, N, K) passes it to
+ * its GEMM kernel (ming-ops.h:84-90, ming-ops.cc:119-141). For dense (bf16)
+ * weights, that linear's kind: a quantized weight is refused (MING_ERR_ARG;
+ * ming_lin then ming_bias_act adds a bias after the rounding). bias [N] bf16
+ * on the device; the other arguments as ming_lin's. */
+int ming_lin_bias(ming_ctx* ctx, const ming_qweight* qw, const uint16_t* x,
+                  int64_t ldx, uint16_t* y, int64_t ldy, int M,
+                  const float* scales, const uint16_t* bias);
+
 /* ming_lin that allocates nothing. It has NO counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same

@@ -121,7 +121,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
 #pragma unroll
     for (int m = 0; m < kGemvMaxM; ++m)
       if (m < a.M) {
-        const float v = ((red[0][m][lane] + red[1][m][lane]) + red[2][m][lane]) + red[3][m][lane];
+        float v = ((red[0][m][lane] + red[1][m][lane]) + red[2][m][lane]) + red[3][m][lane];
+        if (a.bias) v += bf16_to_f32(a.bias[n]);
         a.y[(long long)m * a.ldy + n] = (uint16_t)f32_to_bf16_bits(v);
       }
   }

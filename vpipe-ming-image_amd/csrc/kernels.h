@@ -72,6 +72,9 @@ struct QprojArgs {
   const uint32_t* codes_u;
   const uint32_t* sb_u;
   QprojSeg seg_u;
+  // optional bias [N] bf16, added to the f32 result before the output's one
+  // bf16 rounding (the general kernel: a dense weight's ming_lin_bias)
+  const uint16_t* bias;
 };
 
 // wide: bits 4/8 run with bf16 activations and the weight as a bf16 pair
@@ -133,6 +136,9 @@ struct LoraXaArgs {
   uint16_t* xh;
   long long ldxh;
   int* range;
+  // optional (fast kernel only): bias [n_cols] bf16, T = bf16(coef * sum +
+  // bias) -- the dense split-K GEMM's ming_lin_bias
+  const uint16_t* bias;
 };
 hipError_t launch_lora_xa(const LoraXaArgs& a, hipStream_t s);
 
@@ -239,6 +245,7 @@ struct GemvArgs {
   uint16_t* y;
   long long ldy;
   int M, N, K;
+  const uint16_t* bias;   // optional bias [N] bf16, added before the rounding
 };
 hipError_t launch_gemv(int bits, const GemvArgs& a, hipStream_t s);
 // Up to kGemvBatch GEMVs of one shape over one x in one launch (grid y =

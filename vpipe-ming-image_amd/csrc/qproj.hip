@@ -361,9 +361,16 @@ __global__ __launch_bounds__(NT, 1) void qproj_kernel(const QprojArgs a) {
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + 128 * wn + 32 * j + 8 * q + 4 * fk;
         if (m < a.M && n < a.N) {
+          float r[4] = {acc[j][i][4 * q + 0], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2],
+                        acc[j][i][4 * q + 3]};
+          if (a.bias) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < a.N) r[e] += bf16_to_f32(a.bias[n + e]);
+          }
           uint2 v;
-          v.x = pack_bf16x2_rne(acc[j][i][4 * q + 0], acc[j][i][4 * q + 1]);
-          v.y = pack_bf16x2_rne(acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
+          v.x = pack_bf16x2_rne(r[0], r[1]);
+          v.y = pack_bf16x2_rne(r[2], r[3]);
           *reinterpret_cast<uint2*>(a.y + (long long)m * a.ldy + n) = v;
         }
       }

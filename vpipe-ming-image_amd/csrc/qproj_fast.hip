@@ -1007,6 +1007,13 @@ __global__ __launch_bounds__(512, 1) void lora_xa_fast_kernel(const LoraXaArgs a
         uint2 v;
         if (f == 0.0f) {
           v = make_uint2(0, 0);
+        } else if (a.bias) {
+          // the dense split-K GEMM with a bias (coef 1): one rounding
+          float r[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r[e] = f * acc[i][j][4 * q + e] + bf16_to_f32(a.bias[c + e]);
+          v.x = pack_bf16x2_rne(r[0], r[1]);
+          v.y = pack_bf16x2_rne(r[2], r[3]);
         } else {
           v.x = pack_bf16x2_rne(f * acc[i][j][4 * q + 0], f * acc[i][j][4 * q + 1]);
           v.y = pack_bf16x2_rne(f * acc[i][j][4 * q + 2], f * acc[i][j][4 * q + 3]);
@@ -1053,7 +1060,17 @@ __global__ void lora_xa_reduce_kernel(const float* part, int kslices, int M,
     }
     const float co = a.coef[c >> 3];
     uint4 o = make_uint4(0, 0, 0, 0);
-    if (co != 0.0f) {
+    if (co != 0.0f && a.bias) {
+      // the dense split-K GEMM with a bias (coef 1): one rounding
+      float r[8] = {co * s0.x, co * s0.y, co * s0.z, co * s0.w,
+                    co * s1.x, co * s1.y, co * s1.z, co * s1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] += bf16_to_f32(a.bias[c + e]);
+      o.x = pack_bf16x2_rne(r[0], r[1]);
+      o.y = pack_bf16x2_rne(r[2], r[3]);
+      o.z = pack_bf16x2_rne(r[4], r[5]);
+      o.w = pack_bf16x2_rne(r[6], r[7]);
+    } else if (co != 0.0f) {
       o.x = pack_bf16x2_rne(co * s0.x, co * s0.y);
       o.y = pack_bf16x2_rne(co * s0.z, co * s0.w);
       o.z = pack_bf16x2_rne(co * s1.x, co * s1.y);

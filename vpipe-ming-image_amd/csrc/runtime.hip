@@ -825,6 +825,7 @@ struct LinOut {
   int64_t ldg = 0;
   uint16_t* yh = nullptr;
   bool* took_fast = nullptr;
+  const uint16_t* bias = nullptr;   // dense weights only (ming_lin_bias)
 };
 
 // n projections over the same x [M][K] (q, k, v; w1, w3): x is converted to
@@ -895,7 +896,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
       for (int i = 0; i < n; ++i) {
         const ming_qweight* q = qs[i];
         const ming::GemvArgs ga{x, ldx, q->codes_t, q->sb, q->w16, outs[i].y, outs[i].ldy,
-                                M, q->N, K};
+                                M, q->N, K, outs[i].bias};
         const double wbytes = q->bits == 16
                                   ? 2.0 * q->N * K
                                   : (double)q->N * K * q->bits / 8 + 4.0 * q->N * (K / 64);
@@ -1177,6 +1178,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     a.g = nullptr; a.ldg = 0;
     a.yh = nullptr; a.ldyh = 0;
     a.range = range_word(c);
+    a.bias = o.bias;   // set for dense weights only: the general kernel adds it
     if (o.gate && !fast[i]) {
       a.y = up; a.ldy = q->N;
     }
@@ -1198,7 +1200,7 @@ static int lin_multi(ming_ctx* c, int n, const ming_qweight* const* qs, const Li
     if (dense_ks[i] > 0) {
       ming::LoraXaArgs da{};
       da.x = x; da.ldx = ldx; da.A[0] = q->w16; da.K = K; da.M = M;
-      da.n_cols = q->N; da.t = o.y; da.ldt = (int)o.ldy;
+      da.n_cols = q->N; da.t = o.y; da.ldt = (int)o.ldy; da.bias = o.bias;
       for (int gi = 0; gi < q->N / 8; ++gi) {
         da.grp[gi] = (int16_t)gi;
         da.coef[gi] = 1.0f;
@@ -1255,6 +1257,21 @@ int ming_lin(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,
              int64_t ldx, uint16_t* y, int64_t ldy, int M,
              const float* scales) {
   return lin_impl(c, qc, x, ldx, y, ldy, M, scales, nullptr, 0, nullptr, nullptr);
+}
+
+int ming_lin_bias(ming_ctx* c, const ming_qweight* qc, const uint16_t* x, int64_t ldx,
+                  uint16_t* y, int64_t ldy, int M, const float* scales, const uint16_t* bias) {
+  if (!c || !qc || !bias) return fail(MING_ERR_ARG, "ming_lin_bias: null argument");
+  if (qc->bits != 16)
+    return fail(MING_ERR_ARG,
+                "ming_lin_bias: the bias is for dense (bf16) weights, as LlmOps::linear's; "
+                "a quantized weight takes ming_lin and ming_bias_act");
+  if (!aligned(bias, 2)) return fail(MING_ERR_ARG, "ming_lin_bias: bias must be 2-byte aligned");
+  LinOut o;
+  o.y = y;
+  o.ldy = ldy;
+  o.bias = bias;
+  return lin_multi(c, 1, &qc, &o, x, ldx, M, scales, nullptr);
 }
 
 int ming_lin_noalloc(ming_ctx* c, const ming_qweight* qc, const uint16_t* x,

@@ -204,6 +204,7 @@ def lib():
         "ming_qweight_unbind_lora": ([vp, i32, i32], i32),
         "ming_qweight_lora_rank": ([vp, i32, i32], i32),
         "ming_lin": ([vp, vp, vp, i64, vp, i64, i32, C.POINTER(f32)], i32),
+        "ming_lin_bias": ([vp, vp, vp, i64, vp, i64, i32, C.POINTER(f32), vp], i32),
         "ming_lin_noalloc": ([vp, vp, vp, i64, vp, i64, i32, C.POINTER(f32)], i32),
         "ming_rmsnorm": ([vp, vp, i64, vp, vp, i64, i32, i32, f32], i32),
         "ming_rope_table": ([vp, vp, vp, vp, i32, C.POINTER(i32), i32,
@@ -364,6 +365,15 @@ class Ctx:
         ldy = qw.N if ldy is None else ldy
         _check(lib().ming_lin(self.h, qw.h, _ptr(x), ldx, _ptr(y), ldy, M,
                               _scales(scales)))
+
+    def lin_bias(self, qw: "QWeight", x, y, M: int, bias, scales=None, ldx=None,
+                 ldy=None):
+        """ming_lin_bias (LlmOps::linear with a bias): the bias added before
+        the output's one rounding; dense weights."""
+        ldx = qw.K if ldx is None else ldx
+        ldy = qw.N if ldy is None else ldy
+        _check(lib().ming_lin_bias(self.h, qw.h, _ptr(x), ldx, _ptr(y), ldy, M,
+                                   _scales(scales), _ptr(bias)))
 
     def lin_noalloc(self, qw: "QWeight", x, y, M: int, scales=None, ldx=None,
                     ldy=None):
