@@ -33,12 +33,16 @@ def test_zero_rows_launch_and_write_nothing(ctx):
     qkv = _sentinel(8, 3 * 128 * 2)
     tab = torch.zeros((8, 64), dtype=torch.float32, device="cuda")
     nw = to_dev(bf16(1.0 + randn(852, (128,), 0.1)))
+    dpack, _ = make_weight(853, F, H, 16)
+    wd = m.QWeight.dense(ctx, dpack["w"])
+    bias = to_dev(bf16(randn(854, (F,))))
     sync()
     ctx.reset_engagement()
     before = ctx.engagement()
     for route in ("auto", "general", "wide"):
         ctx.set_route(route)
         ctx.lin(ws[0], x, h, 0, CFG2_SCALES)
+        ctx.lin_bias(wd, x, h, 0, bias)
         ctx.lin_noalloc(ws[0], x, h, 0, CFG2_SCALES)
         ctx.lin_swiglu(ws[1], x, h, h, 0, CFG2_SCALES)
         ctx.ffn(ws[0], ws[1], ws[2], x, y, 0, CFG2_SCALES, h=h)
@@ -59,5 +63,8 @@ def test_zero_rows_launch_and_write_nothing(ctx):
         ctx.lin(ws[0], x, h, -1, CFG2_SCALES)
     with pytest.raises(m.MingError):
         ctx.rmsnorm(x, w, y, -1, H)
+    with pytest.raises(m.MingError):
+        ctx.lin_bias(wd, x, h, -1, bias)
     for q in ws:
         q.close()
+    wd.close()
